@@ -1,0 +1,243 @@
+"""Benchmark of the quantized-weight matmul path on one MI355X.
+
+Headline: Q4_K GEMV GB/s (% of HBM peak) at 5120 -> 17408,
+M=1 (configs[1], gate/up shape), plus the prefill GEMM TFLOP/s at M=4096.
+
+A "step" is one Q4_K GEMV over one weight copy: y = W x, W 17408 x 5120 Q4_K
+(50,135,040 B), x F32 5120. Inputs are resident in HBM. The timed region
+replays a HIP graph of back-to-back GEMVs that rotate over enough distinct
+weight copies (>= 512 MB) that every call streams from HBM and not from the
+256 MB Infinity Cache. `value` = weight bytes per step x steps / wall time;
+the roofline uses the algorithmic bytes (weights + x + y) over the average
+launch duration measured with HIP events on the launch stream.
+
+cpu_baseline: the CPU oracle's matvec (the C restatement of nuclis's
+cpu.matvec; the Zig reference cannot be built here) on the same matrix, timed
+on this host with min(64, cores) threads for ~10 s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extras]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--extras", action="store_true", help="also time the other configs (verify, layer, Q6_K)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default="", help="comma list: gemv,prefill")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+        self.start = torch.cuda.Event(enable_timing=True)
+        self.end = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.start.record(self.stream)
+        return self
+
+    def __exit__(self, *exc):
+        self.end.record(self.stream)
+        self.end.synchronize()
+        self.ms = self.start.elapsed_time(self.end)
+
+
+def copies_for(nbytes: int) -> int:
+    return max(8, -(-2 * MALL_BYTES // nbytes))
+
+
+def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmup, seed=2):
+    from nuclis_amd.synth import gaussian
+    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+    x = torch.from_numpy(gaussian(1, columns)).cuda()
+    ncopies = copies_for(w.nbytes)
+    base = torch.from_numpy(w).cuda()
+    mats = [nq.Matrix(encoding, rows, columns, base if i == 0 else base.clone()) for i in range(ncopies)]
+    ys = [torch.empty(rows, device="cuda") for _ in range(ncopies)]
+    with torch.cuda.stream(stream):
+        for i in range(ncopies):
+            backend.matvec(mats[i], x, ys[i])
+        eager = [y.clone() for y in ys]
+        # one graph = one pass over every copy
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(ncopies):
+                backend.matvec(mats[i], x, ys[i])
+        reps = max(1, steps // ncopies)
+        wreps = max(1, warmup // ncopies)
+        for _ in range(wreps):
+            graph.replay()
+        torch.cuda.synchronize()
+        for i in range(ncopies):  # every replay must equal the eager result
+            assert torch.equal(ys[i], eager[i]), "graph replay differs from eager GEMV"
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with Timer(torch, stream) as t:
+            for _ in range(reps):
+                graph.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    launches = reps * ncopies
+    weight_bytes = w.nbytes
+    algo_bytes = weight_bytes + columns * 4 + rows * 4
+    kernel_s = t.ms / 1e3 / launches
+    return {
+        "launches": launches, "copies": ncopies, "wall_s": wall, "event_ms": t.ms,
+        "weight_bytes": weight_bytes, "algo_bytes": algo_bytes,
+        "us_per_launch": kernel_s * 1e6,
+        "weight_gbs": weight_bytes / kernel_s / 1e9,
+        "algo_gbs": algo_bytes / kernel_s / 1e9,
+        "wall_weight_gbs": weight_bytes * launches / wall / 1e9,
+        "w": w, "x": x, "y0": eager[0],
+    }
+
+
+def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps=20, warmup=3, seed=2,
+               kernel=None):
+    from nuclis_amd.synth import gaussian
+    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+    x = torch.from_numpy(gaussian(7, (tokens, columns))).cuda().to(torch.float16)
+    wg = torch.from_numpy(w).cuda()
+    m = nq.Matrix(encoding, rows, columns, wg)
+    y = torch.empty((tokens, rows), device="cuda")
+    k = nq.KERNEL_TILE if kernel is None else kernel
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
+        torch.cuda.synchronize()
+        with Timer(torch, stream) as t:
+            for _ in range(reps):
+                backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
+    s = t.ms / 1e3 / reps
+    flops = 2.0 * tokens * rows * columns
+    return {"ms": s * 1e3, "tflops": flops / s / 1e12, "flops": flops, "weight_gbs": w.nbytes / s / 1e9,
+            "frac_f16_peak": flops / s / 1e12 / F16_PEAK_TFLOPS}
+
+
+def cpu_baseline(w, x_host, rows, columns, seconds):
+    from oracle import oracle as orc
+    threads = orc.default_threads()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        y = orc.matvec(12, rows, columns, w, x_host, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 3:
+            break
+    med = float(np.median(times))
+    return {"value": round(w.nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full Q4_K 17408x5120 matvecs (oracle cpu.matvec restatement, F64 accumulate), "
+                      f"median {med * 1e3:.1f} ms each; host has {os.cpu_count()} logical CPUs",
+            "y": y}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is design-only "
+                                   "(rows split across GPUs, see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    import nuclis_amd as nq
+    torch.cuda.init()
+    backend = nq.Backend(0)
+    stream = torch.cuda.Stream()
+    only = set(filter(None, args.only.split(",")))
+    rows, columns = 17408, 5120
+    out = {}
+    g = bench_gemv(torch, nq, backend, stream, nq.Q4_K, rows, columns, args.steps, args.warmup)
+    # correctness of the timed kernel against the oracle on a row sample
+    from oracle import oracle as orc
+    x_host = g["x"].cpu().numpy()
+    sample = np.arange(0, rows, 97)
+    ref = orc.matvec(12, sample.size, columns, np.ascontiguousarray(g["w"][sample]), x_host)
+    got = g["y0"].cpu().numpy()[sample]
+    normwise = float(np.abs(got - ref).max() / np.abs(ref).max())
+    assert normwise <= 2e-3, normwise
+    prefill = None
+    if not only or "prefill" in only:
+        prefill = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 4096)
+    extras = {}
+    if args.extras:
+        extras["q4k_down_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q4_K, 5120, 17408,
+                                                                 args.steps, args.warmup).items()
+                                   if k not in ("w", "x", "y0")}
+        extras["q6k_lmhead_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q6_K, 151936, 5120,
+                                                                   64, 8).items() if k not in ("w", "x", "y0")}
+        extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
+                                                             args.steps, args.warmup).items()
+                               if k not in ("w", "x", "y0")}
+        extras["prefill_q6k_down_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q6_K, 5120, 17408, 4096)
+        extras["prefill_q4k_gate_m512"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 512)
+        for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
+            extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 8,
+                                                               reps=200, warmup=20, kernel=kid)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(g["w"], x_host, rows, columns, args.cpu_seconds)
+        cpu.pop("y")
+    kernel_s = g["us_per_launch"] / 1e6
+    result = {
+        "metric": "Q4_K GEMV GB/s (% of HBM peak) @5120x17408 M=1; prefill GEMM TFLOPS @M=4096",
+        "value": round(g["wall_weight_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": g["launches"],
+        "warmup": args.warmup,
+        "ms_per_step": round(g["wall_s"] * 1e3 / g["launches"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x f32 -> f32 (fp32 accumulate)",
+        "data": "synthetic: W ~ N(0,0.02) seed 2 quantized to Q4_K by libnuq, x ~ N(0,1) seed 1",
+        "config": {"workload": "configs[1]: Q4_K batch-1 GEMV gate/up 5120->17408 (N=17408, K=5120), "
+                               f"{g['copies']} rotating weight copies",
+                   "weight_bytes": g["weight_bytes"], "hbm_peak_frac": round(g["wall_weight_gbs"] / HBM_PEAK_GBS, 4),
+                   "parity_normwise": normwise},
+        "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gemv_q4k_kernel<4>",
+                     "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
+        "cpu_baseline": cpu,
+    }
+    if prefill is not None:
+        result["prefill"] = {"workload": "configs[4]: Q4_K 17408x5120, M=4096, f16 activations",
+                             "tflops": round(prefill["tflops"], 2), "ms": round(prefill["ms"], 4),
+                             "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
+                                          "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                          "frac": round(prefill["frac_f16_peak"], 4)}}
+    if extras:
+        result["extras"] = extras
+    backend.close()
+    print(json.dumps(result, default=float))
+
+
+if __name__ == "__main__":
+    main()

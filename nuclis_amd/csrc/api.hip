@@ -1,0 +1,363 @@
+// C-ABI shim of libnuq.so (declared in include/nuq.h): validation with the
+// reference's shape rules, routing, and launches on the context's stream.
+//
+// Validation mirrors, before anything is launched or written:
+//   matvec       backends/metal/ops/matvec.zig:85-89
+//   matvecRows   ops/matvec.zig:149-157
+//   matmul       ops/matmul.zig:77-83
+//   embed        ops/rowwise.zig:17-21
+//   segments     ops/matvec.zig:265-311
+//   validateRow  quant/decode.zig:108-120
+// Routing mirrors the reference's specialised-vs-generic choice
+// (ops/matvec.zig:196-219, ops/matmul.zig:114-123): the vectorised kernels
+// need 16-byte aligned Q4_K rows (pointer and stride), even Q6_K / Q8_0 rows
+// and a 16-byte aligned input; anything else runs the generic control.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/nuq.h"
+#include "formats.h"
+#include "kernels.h"
+
+struct nuq_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool generic_only = false;
+    std::string last_error;
+    uint32_t *argmax_buf = nullptr;  // device: {index, nonfinite flag}
+};
+
+namespace {
+
+int fail(nuq_context *ctx, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+int fail(nuq_context *ctx, int code, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->last_error = buf;
+    }
+    return code;
+}
+
+int hip_check(nuq_context *ctx, hipError_t e, const char *what) {
+    if (e == hipSuccess) return NUQ_OK;
+    return fail(ctx, NUQ_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+int validate_row(uint32_t encoding, uint64_t byte_count, uint64_t element_count) {
+    nuq::Layout l;
+    if (!nuq::layout_of(encoding, &l)) return NUQ_UNSUPPORTED_ENCODING;
+    if (element_count == 0 || element_count % l.elements != 0) return NUQ_INVALID_ROW_LENGTH;
+    if (byte_count % l.bytes != 0 || byte_count / l.bytes != element_count / l.elements) return NUQ_INVALID_BYTE_LENGTH;
+    return NUQ_OK;
+}
+
+const char *status_name(int code) {
+    switch (code) {
+    case NUQ_INVALID_SHAPE: return "InvalidShape";
+    case NUQ_UNSUPPORTED_ENCODING: return "UnsupportedTensorEncoding";
+    case NUQ_INVALID_ROW_LENGTH: return "InvalidRowLength";
+    case NUQ_INVALID_BYTE_LENGTH: return "InvalidByteLength";
+    default: return "error";
+    }
+}
+
+// Shared matrix checks: descriptor present, rows and bytes consistent, whole
+// blocks per row. Returns the row stride in *stride.
+int check_matrix(nuq_context *ctx, const nuq_matrix *m, uint64_t *stride) {
+    if (!m) return fail(ctx, NUQ_INVALID_ARGUMENT, "null matrix");
+    if (m->rows == 0 || m->columns == 0) return fail(ctx, NUQ_INVALID_SHAPE, "empty matrix");
+    if (m->byte_len % m->rows != 0) return fail(ctx, NUQ_INVALID_SHAPE, "byte length not a whole number of rows");
+    *stride = m->byte_len / m->rows;
+    int e = validate_row(m->encoding, *stride, m->columns);
+    if (e) return fail(ctx, e, "%s: encoding %u, %llu bytes per row, %llu columns", status_name(e), m->encoding,
+                       (unsigned long long)*stride, (unsigned long long)m->columns);
+    if (!m->bytes) return fail(ctx, NUQ_INVALID_ARGUMENT, "null weights");
+    if (m->rows > 0x7fffffffull || m->columns > 0x7fffffffull)
+        return fail(ctx, NUQ_INVALID_SHAPE, "matrix dimensions exceed 2^31");
+    return NUQ_OK;
+}
+
+// Whether the vectorised kernels may read this weight range and input
+// (the reference's blockAligned plus its float4 input rule).
+bool vector_aligned(const nuq_matrix *m, uint64_t stride, const void *x) {
+    uintptr_t wp = (uintptr_t)m->bytes;
+    uint64_t need = m->encoding == NUQ_Q4_K ? 16 : 2;
+    return wp % need == 0 && stride % need == 0 && ((uintptr_t)x % 16) == 0;
+}
+
+// Rows per wave of the M=1 GEMV: the number of rows a wave keeps in flight
+// against one register copy of its x slice.
+int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
+    if (encoding == NUQ_Q6_K) return rows >= 65536 ? 4 : 2;
+    if (encoding == NUQ_Q8_0) return 2;
+    return rows >= 8192 ? 4 : 2;
+}
+
+int run_generic(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const void *x, uint32_t x_f16,
+                uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
+    return hip_check(ctx,
+                     nuq::launch_generic(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                         (uint32_t)m->columns, x, x_f16, in_stride, out, out_stride, tokens),
+                     "generic kernel launch");
+}
+
+int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const void *x, uint32_t x_dtype,
+                uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    uint64_t stride;
+    int e = check_matrix(ctx, m, &stride);
+    if (e) return e;
+    // ops/matmul.zig:77-83
+    if (m->rows % 8 != 0 || m->columns % 64 != 0)
+        return fail(ctx, NUQ_INVALID_SHAPE, "matmul needs rows %% 8 == 0 and columns %% 64 == 0");
+    if (tokens == 0 || in_stride < m->columns || out_stride < m->rows)
+        return fail(ctx, NUQ_INVALID_SHAPE, "matmul: tokens, in_stride or out_stride out of range");
+    if (x_dtype != NUQ_F32 && x_dtype != NUQ_F16) return fail(ctx, NUQ_INVALID_ARGUMENT, "unknown activation dtype");
+    if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null activation or output");
+    const uint64_t elem = x_dtype == NUQ_F16 ? 2 : 4;
+    if ((uintptr_t)x % 16 != 0 || (in_stride * elem) % 16 != 0 || (uintptr_t)out % 4 != 0)
+        return fail(ctx, NUQ_INVALID_SHAPE, "matmul: activations must be 16-byte aligned rows");
+    if (kernel > NUQ_KERNEL_GENERIC) return fail(ctx, NUQ_INVALID_ARGUMENT, "unknown kernel %u", kernel);
+    if (kernel == NUQ_KERNEL_ROWS && tokens > 8)
+        return fail(ctx, NUQ_INVALID_SHAPE, "the multi-token GEMV serves at most 8 tokens");
+    const uint32_t f16 = x_dtype == NUQ_F16;
+    const bool aligned = vector_aligned(m, stride, x);
+    if (ctx->generic_only || kernel == NUQ_KERNEL_GENERIC || !aligned)
+        return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
+    if (kernel == NUQ_KERNEL_AUTO) {
+        if (tokens == 1 && !f16) {
+            return hip_check(ctx,
+                             nuq::launch_gemv(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                              (uint32_t)m->rows, (uint32_t)m->columns, (const float *)x, out,
+                                              gemv_rows_per_wave(m->encoding, m->rows)),
+                             "gemv launch");
+        }
+        kernel = tokens <= 3 ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
+    }
+    if (kernel == NUQ_KERNEL_ROWS)
+        return hip_check(ctx,
+                         nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                          (uint32_t)m->rows, (uint32_t)m->columns, x, f16, in_stride, out,
+                                          out_stride, tokens),
+                         "multi-token gemv launch");
+    return hip_check(ctx,
+                     nuq::launch_tile(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                      (uint32_t)m->columns, x, f16, in_stride, out, out_stride, tokens),
+                     "tile launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+nuq_context *nuq_create(int device, char *err, size_t cap) {
+    auto report = [&](const char *msg) {
+        if (err && cap) {
+            std::snprintf(err, cap, "%s", msg);
+        }
+    };
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        report("no HIP device available");
+        return nullptr;
+    }
+    if (device < 0 || device >= count) {
+        report("device index out of range");
+        return nullptr;
+    }
+    if (hipSetDevice(device) != hipSuccess) {
+        report("hipSetDevice failed");
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess || std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        char msg[256];
+        std::snprintf(msg, sizeof msg, "libnuq is built for gfx950; device %d is %s", device, prop.gcnArchName);
+        report(msg);
+        return nullptr;
+    }
+    auto *ctx = new nuq_context();
+    ctx->device = device;
+    if (hipMalloc((void **)&ctx->argmax_buf, 2 * sizeof(uint32_t)) != hipSuccess) {
+        report("hipMalloc of the argmax result failed");
+        delete ctx;
+        return nullptr;
+    }
+    return ctx;
+}
+
+void nuq_destroy(nuq_context *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->argmax_buf) (void)hipFree(ctx->argmax_buf);
+    delete ctx;
+}
+
+int nuq_set_stream(nuq_context *ctx, void *stream) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    ctx->stream = (hipStream_t)stream;
+    return NUQ_OK;
+}
+
+int nuq_sync(nuq_context *ctx) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    (void)hipSetDevice(ctx->device);
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+}
+
+const char *nuq_last_error(const nuq_context *ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
+
+int nuq_set_generic_only(nuq_context *ctx, int enabled) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    ctx->generic_only = enabled != 0;
+    return NUQ_OK;
+}
+
+int nuq_validate_row(uint32_t encoding, uint64_t byte_count, uint64_t element_count) {
+    return validate_row(encoding, byte_count, element_count);
+}
+
+int nuq_dequant_rows(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uint64_t count, float *out) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    uint64_t stride;
+    int e = check_matrix(ctx, m, &stride);
+    if (e) return e;
+    if (m->columns % 16 != 0) return fail(ctx, NUQ_INVALID_SHAPE, "columns must be a multiple of 16");
+    if (count == 0 || first >= m->rows || count > m->rows - first)
+        return fail(ctx, NUQ_INVALID_SHAPE, "row range outside the matrix");
+    if (count > 0xffffffffull) return fail(ctx, NUQ_INVALID_SHAPE, "too many rows in one call");
+    if (!out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null output");
+    return hip_check(ctx,
+                     nuq::launch_dequant_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, first,
+                                              (uint32_t)count, (uint32_t)m->columns, out),
+                     "dequant launch");
+}
+
+int nuq_embed(nuq_context *ctx, const nuq_matrix *m, uint32_t token, float *out) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (m && token >= m->rows) return fail(ctx, NUQ_INVALID_SHAPE, "token %u outside %llu rows", token,
+                                           (unsigned long long)m->rows);
+    return nuq_dequant_rows(ctx, m, token, 1, out);
+}
+
+int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    uint64_t stride;
+    int e = check_matrix(ctx, m, &stride);
+    if (e) return e;
+    if (m->columns % 16 != 0) return fail(ctx, NUQ_INVALID_SHAPE, "columns must be a multiple of 16");
+    if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
+    if ((uintptr_t)x % 4 != 0 || (uintptr_t)out % 4 != 0)
+        return fail(ctx, NUQ_INVALID_SHAPE, "input and output must be 4-byte aligned");
+    if (ctx->generic_only || !vector_aligned(m, stride, x))
+        return run_generic(ctx, m, stride, x, 0, m->columns, out, m->rows, 1);
+    return hip_check(ctx,
+                     nuq::launch_gemv(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                      (uint32_t)m->columns, x, out, gemv_rows_per_wave(m->encoding, m->rows)),
+                     "gemv launch");
+}
+
+int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint64_t in_stride, float *out,
+                    uint64_t out_stride, uint32_t tokens) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    uint64_t stride;
+    int e = check_matrix(ctx, m, &stride);
+    if (e) return e;
+    if (m->columns % 16 != 0) return fail(ctx, NUQ_INVALID_SHAPE, "columns must be a multiple of 16");
+    if (tokens < 2 || tokens > 8) return fail(ctx, NUQ_INVALID_SHAPE, "matvecRows serves 2..8 tokens");
+    if (in_stride < m->columns || out_stride < m->rows)
+        return fail(ctx, NUQ_INVALID_SHAPE, "in_stride or out_stride too small");
+    if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
+    if ((uintptr_t)x % 16 != 0 || in_stride % 4 != 0 || (uintptr_t)out % 4 != 0)
+        return fail(ctx, NUQ_INVALID_SHAPE, "input must be float4 aligned (offset and stride)");
+    if (ctx->generic_only || !vector_aligned(m, stride, x))
+        return run_generic(ctx, m, stride, x, 0, in_stride, out, out_stride, tokens);
+    return hip_check(ctx,
+                     nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                      (uint32_t)m->columns, x, 0, in_stride, out, out_stride, tokens),
+                     "multi-token gemv launch");
+}
+
+int nuq_matmul(nuq_context *ctx, const nuq_matrix *m, const void *x, uint32_t x_dtype, uint64_t in_stride, float *out,
+               uint64_t out_stride, uint32_t tokens) {
+    return matmul_impl(ctx, NUQ_KERNEL_AUTO, m, x, x_dtype, in_stride, out, out_stride, tokens);
+}
+
+int nuq_matmul_kernel(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const void *x, uint32_t x_dtype,
+                      uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
+    return matmul_impl(ctx, kernel, m, x, x_dtype, in_stride, out, out_stride, tokens);
+}
+
+int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (!segments || count == 0 || count > 4) return fail(ctx, NUQ_INVALID_SHAPE, "segments: 1..4 projections");
+    if (mode > NUQ_SEGMENT_SILU_MUL_PAIR) return fail(ctx, NUQ_INVALID_ARGUMENT, "unknown segment mode");
+    if (!x || (uintptr_t)x % 16 != 0) return fail(ctx, NUQ_INVALID_SHAPE, "input must be 16-byte aligned");
+    const uint64_t columns = segments[0].matrix.columns;
+    if (columns == 0 || columns % 16 != 0) return fail(ctx, NUQ_INVALID_SHAPE, "columns must be a multiple of 16");
+    if (mode != NUQ_SEGMENT_PLAIN &&
+        (count != 2 || segments[0].matrix.rows != segments[1].matrix.rows || segments[0].output != segments[1].output))
+        return fail(ctx, NUQ_INVALID_SHAPE, "a pair needs two segments of equal rows naming one output");
+    nuq::SegmentsArgs args;
+    std::memset(&args, 0, sizeof args);
+    args.count = count;
+    args.mode = mode;
+    const uint32_t rpw = (uint32_t)nuq::segment_rows_per_wave();
+    uint32_t waves = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const nuq_matrix &m = segments[i].matrix;
+        uint64_t stride;
+        int e = check_matrix(ctx, &m, &stride);
+        if (e) return e;
+        if (m.rows % 16 != 0 || m.columns != columns)
+            return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: rows %% 16 and equal columns required", i);
+        if (!segments[i].output || (uintptr_t)segments[i].output % 4 != 0)
+            return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: output null or misaligned", i);
+        if (!vector_aligned(&m, stride, x))
+            return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: weights not aligned for the merged kernel", i);
+        // Plain outputs must be disjoint from each other and from the input.
+        const float *o = segments[i].output;
+        if ((const void *)o < (const void *)(x + columns) && (const void *)x < (const void *)(o + m.rows))
+            return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: output overlaps the input", i);
+        if (mode == NUQ_SEGMENT_PLAIN)
+            for (uint32_t k = 0; k < i; ++k) {
+                const float *p = segments[k].output;
+                if (o < p + segments[k].matrix.rows && p < o + m.rows)
+                    return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: output overlaps segment %u", i, k);
+            }
+        nuq::Layout l;
+        nuq::layout_of(m.encoding, &l);
+        args.seg[i] = {(const uint8_t *)m.bytes, stride, segments[i].output, m.encoding, (uint32_t)m.rows,
+                       (uint32_t)(columns / l.elements), 0};
+        args.wave_start[i] = waves;
+        waves += (uint32_t)((m.rows + rpw - 1) / rpw);
+    }
+    args.wave_start[count] = waves;
+    if (mode != NUQ_SEGMENT_PLAIN) args.wave_start[1] = (uint32_t)((segments[0].matrix.rows + rpw - 1) / rpw);
+    return hip_check(ctx, nuq::launch_segments(ctx->stream, args, x), "segments launch");
+}
+
+int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *index) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (!logits || !index) return fail(ctx, NUQ_INVALID_ARGUMENT, "null logits or index");
+    if (count == 0 || count > 0xffffffffull) return fail(ctx, NUQ_INVALID_SHAPE, "logit count out of range");
+    int e = hip_check(ctx, nuq::launch_argmax(ctx->stream, logits, count, ctx->argmax_buf), "argmax launch");
+    if (e) return e;
+    uint32_t host[2];
+    e = hip_check(ctx, hipMemcpyAsync(host, ctx->argmax_buf, sizeof host, hipMemcpyDeviceToHost, ctx->stream),
+                  "argmax readback");
+    if (e) return e;
+    e = hip_check(ctx, hipStreamSynchronize(ctx->stream), "argmax synchronize");
+    if (e) return e;
+    if (host[1]) return fail(ctx, NUQ_NON_FINITE, "NonFiniteResult: a logit is not finite");
+    *index = host[0];
+    return NUQ_OK;
+}
+
+}  // extern "C"

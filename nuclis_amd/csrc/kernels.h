@@ -1,0 +1,43 @@
+// Launchers shared between the kernel translation units and the C-ABI shim.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nuq {
+
+struct SegmentDesc {
+    const uint8_t *w;
+    uint64_t stride;
+    float *out;
+    uint32_t encoding;
+    uint32_t rows;
+    uint32_t nblocks;
+    uint32_t pad;
+};
+
+struct SegmentsArgs {
+    SegmentDesc seg[4];
+    uint32_t wave_start[5];  // prefix sums of each segment's wave count
+    uint32_t count;
+    uint32_t mode;  // 0 plain, 1 silu(seg0) * seg1
+};
+
+hipError_t launch_dequant_rows(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint64_t first,
+                               uint32_t count, uint32_t columns, float *out);
+hipError_t launch_gemv(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                       uint32_t columns, const float *x, float *y, int rows_per_wave);
+hipError_t launch_generic(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                          uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                          uint64_t out_stride, uint32_t tokens);
+hipError_t launch_rows(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                       uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                       uint64_t out_stride, uint32_t tokens);
+hipError_t launch_segments(hipStream_t s, const SegmentsArgs &args, const float *x);
+int segment_rows_per_wave();
+hipError_t launch_argmax(hipStream_t s, const float *logits, uint64_t count, uint32_t *result);
+hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                       uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                       uint64_t out_stride, uint32_t tokens);
+
+}  // namespace nuq

@@ -1,0 +1,45 @@
+"""Helpers of the GPU parity tests: device upload and the tolerance checks.
+
+Tolerances (stated where they are used):
+  * dequantisation: bit-exact against the oracle decoder;
+  * F32-arithmetic products (GEMV, multi-token GEMV, generic control):
+    |gpu - ref| <= 4e-6 * sum|w*x| + 1e-6 per output, the reference's bound
+    for its matvecs (metal-check.zig:3976), and normwise
+    max|gpu - ref| / max|ref| <= 2e-3 (the stated max relative error);
+  * f16 MFMA tile: weights (and F32 activations) are rounded to f16, each
+    term then carries at most 2^-11 relative error per rounded operand, so
+    |gpu - ref| <= 2e-3 * sum|w*x| + 1e-6 per output, plus the same 2e-3
+    normwise bound.
+"""
+import numpy as np
+
+from oracle import oracle as orc
+
+
+def to_gpu(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def mass(encoding, w_bytes, rows, columns, x):
+    """sum_c |w[r,c] * x[t,c]| for every token t and row r (F64)."""
+    dec = orc.decode_matrix(encoding, w_bytes, rows, columns).astype(np.float64)
+    return np.abs(np.atleast_2d(x).astype(np.float64)) @ np.abs(dec).T
+
+
+def check_close(got, want, mass_, k, label=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert np.all(np.isfinite(got)), f"{label}: non-finite output"
+    err = np.abs(got - want)
+    bound = k * mass_ + 1e-6
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert np.all(err <= bound), (f"{label}: |d|={err[worst]:.3e} > bound {bound[worst]:.3e} at {worst} "
+                                  f"(got {got[worst]}, want {want[worst]})")
+    normwise = err.max() / max(np.abs(want).max(), 1e-30)
+    assert normwise <= 2e-3, f"{label}: normwise {normwise:.3e}"
+    return normwise

@@ -1,0 +1,334 @@
+"""Parity of the HIP path (libnuq.so on cuda:0) with the CPU oracle.
+
+Inputs are seeded (nuclis_amd.synth.gaussian: numpy PCG64, N(0,0.02) weights,
+N(0,1) activations) and quantized by libnuq's host quantizers; the oracle and
+the GPU read the same bytes. Tolerances are documented in tests/gpu_util.py.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import nuclis_amd as nq
+from nuclis_amd.synth import gaussian
+from oracle import oracle as orc
+from tests.gpu_util import check_close, mass, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "decoder_fixtures.json").read_text())
+F32_K = 4e-6   # reference matvec bound (metal-check.zig:3976)
+F16_K = 2e-3   # f16-rounded operands
+
+
+@pytest.fixture(scope="module")
+def backend():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    b = nq.Backend(0)
+    yield b
+    b.close()
+
+
+def fixture_blocks(encoding):
+    for row in GOLDEN["rows"]:
+        if row["encoding"] == encoding:
+            return np.frombuffer(bytes.fromhex(row["bytes_hex"]), np.uint8), \
+                np.frombuffer(bytes.fromhex(row["values_f32_hex"]), np.float32)
+
+
+def tiled(encoding, rows, columns):
+    """metal-check.zig:284-302 (tiledMatrix): block (r*3+t) % n of the fixture."""
+    raw, _ = fixture_blocks(encoding)
+    n, size = nq.LAYOUT[encoding]
+    blocks = raw.reshape(-1, size)
+    per_row = columns // n
+    idx = (np.arange(rows)[:, None] * 3 + np.arange(per_row)[None, :]) % len(blocks)
+    return np.ascontiguousarray(blocks[idx].reshape(rows, per_row * size))
+
+
+def tame(w, encoding):
+    """metal-check.zig:329-345 (tameScales): F16 scales set to 2^-6."""
+    n, size = nq.LAYOUT[encoding]
+    b = w.reshape(-1, size).copy()
+    positions = {12: (0, 2), 14: (208,), 8: (0,)}[encoding]
+    for p in positions:
+        b[:, p] = 0x00
+        b[:, p + 1] = 0x24
+    return b.reshape(w.shape)
+
+
+def quantized(encoding, rows, columns, seed):
+    return nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+
+
+# ---------------------------------------------------------------- dequant
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_embed_fixture_rows_bit_exact(backend, encoding):
+    import torch
+    raw, values = fixture_blocks(encoding)
+    n = nq.LAYOUT[encoding][0]
+    rows = values.size // n
+    w = to_gpu(raw)
+    m = nq.Matrix(encoding, rows, n, w)
+    for token in range(rows):
+        out = torch.empty(n, dtype=torch.float32, device="cuda")
+        backend.embed(m, token, out)
+        backend.sync()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), values[token * n:(token + 1) * n].view(np.uint32))
+
+
+@pytest.mark.parametrize("encoding,rows,columns", [(8, 96, 4096), (12, 64, 5120), (14, 40, 17408), (12, 35, 17408)])
+def test_dequant_rows_bit_exact_tiled_and_random(backend, encoding, rows, columns):
+    import torch
+    for w in (tiled(encoding, rows, columns), quantized(encoding, rows, columns, 7)):
+        out = torch.empty(rows * columns, dtype=torch.float32, device="cuda")
+        backend.dequant_rows(nq.Matrix(encoding, rows, columns, to_gpu(w)), 0, rows, out)
+        backend.sync()
+        want = orc.decode_matrix(encoding, w, rows, columns)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.ravel().view(np.uint32))
+
+
+def test_dequant_subnormal_q4_k_scales_bit_exact(backend):
+    import torch
+    b = np.zeros((4, 144), np.uint8)
+    b[:, 0:4] = [[1, 0, 3, 0], [0xff, 0x03, 0x01, 0x80], [0, 0x04, 0x10, 0], [0x55, 0x02, 0x00, 0x01]]
+    b[:, 4:16] = np.arange(12, dtype=np.uint8) * 21
+    b[:, 16:] = np.arange(128, dtype=np.uint8)
+    out = torch.empty(4 * 256, dtype=torch.float32, device="cuda")
+    backend.dequant_rows(nq.Matrix(12, 4, 256, to_gpu(b)), 0, 4, out)
+    backend.sync()
+    want = orc.decode_matrix(12, b, 4, 256)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.ravel().view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMV M=1
+GEMV_SHAPES = [
+    (8, 4096, 4096),      # config 1
+    (12, 17408, 5120),    # config 2 gate/up
+    (12, 5120, 17408),    # config 2 down
+    (12, 1024, 5120),     # k/v
+    (12, 5120, 6144),     # o
+    (14, 4096, 5120),     # lm_head slice
+    (14, 5120, 17408),    # prefill down shape
+    (12, 35, 1280),       # ragged rows (metal-check randomized rows)
+    (14, 35, 1280),
+    (8, 35, 1280),
+    (12, 1, 256),
+]
+
+
+@pytest.mark.parametrize("encoding,rows,columns", GEMV_SHAPES)
+def test_matvec_matches_oracle(backend, encoding, rows, columns):
+    import torch
+    w = quantized(encoding, rows, columns, 100 + rows % 97)
+    x = gaussian(1, columns)
+    out = torch.full((rows,), np.nan, dtype=torch.float32, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    want = orc.matvec(encoding, rows, columns, w, x)
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"matvec {encoding}")
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_matvec_tiled_fixture_blocks_and_basis_columns(backend, encoding):
+    """Fixture blocks (extreme real scales) tiled into 35 x 1280; plus one-hot
+    inputs that select decoded columns (cpu/root.zig:240-272)."""
+    import torch
+    rows, columns = 35, 1280
+    w = tiled(encoding, rows, columns)
+    wg = to_gpu(w)
+    m = nq.Matrix(encoding, rows, columns, wg)
+    x = gaussian(2, columns)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    backend.matvec(m, to_gpu(x), out)
+    backend.sync()
+    check_close(out.cpu().numpy(), orc.matvec(encoding, rows, columns, w, x), mass(encoding, w, rows, columns, x)[0],
+                F32_K, "tiled")
+    dec = orc.decode_matrix(encoding, w, rows, columns)
+    for column in (0, columns // 2 + 1, columns - 1):
+        e = np.zeros(columns, np.float32)
+        e[column] = 1
+        backend.matvec(m, to_gpu(e), out)
+        backend.sync()
+        got = out.cpu().numpy()
+        assert np.all(np.abs(got - dec[:, column]) <= 1e-5 * np.abs(dec[:, column])), column
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_generic_control_and_misaligned_weights(backend, encoding):
+    import torch
+    rows, columns = 48, 1024
+    w = quantized(encoding, rows, columns, 3)
+    x = gaussian(4, columns)
+    want = orc.matvec(encoding, rows, columns, w, x)
+    mm = mass(encoding, w, rows, columns, x)[0]
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    backend.set_generic_only(True)
+    try:
+        backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+        backend.sync()
+    finally:
+        backend.set_generic_only(False)
+    check_close(out.cpu().numpy(), want, mm, F32_K, "generic")
+    # weights at an odd byte offset: routed to the generic kernel
+    buf = torch.zeros(w.size + 1, dtype=torch.uint8, device="cuda")
+    buf[1:] = to_gpu(w.ravel())
+    backend.matvec(nq.Matrix(encoding, rows, columns, buf[1:]), to_gpu(x), out)
+    backend.sync()
+    check_close(out.cpu().numpy(), want, mm, F32_K, "misaligned")
+
+
+def test_matvec_refusals_leave_output_untouched(backend):
+    import torch
+    w = to_gpu(np.zeros(68, np.uint8))
+    x = to_gpu(np.zeros(32, np.float32))
+    out = torch.full((2,), 123.0, device="cuda")
+    with pytest.raises(nq.InvalidShape):
+        backend.matvec(nq.Matrix(8, 0, 32, w), x, out)
+    with pytest.raises(nq.InvalidShape):
+        backend.matvec(nq.Matrix(8, 2, 32, w, 67), x, out)
+    with pytest.raises(nq.InvalidByteLength):
+        backend.matvec(nq.Matrix(8, 2, 32, w, 66), x, out)
+    with pytest.raises(nq.InvalidRowLength):
+        backend.matvec(nq.Matrix(8, 2, 16, w, 68), x, out)
+    with pytest.raises(nq.UnsupportedTensorEncoding):
+        backend.matvec(nq.Matrix(999, 2, 32, w), x, out)
+    backend.sync()
+    assert out.cpu().tolist() == [123.0, 123.0]
+
+
+# ---------------------------------------------------------------- multi-token
+@pytest.mark.parametrize("encoding,rows,columns", [(12, 2048, 5120), (14, 1024, 5120), (8, 512, 4096),
+                                                   (12, 512, 17408)])
+@pytest.mark.parametrize("tokens", [2, 3, 5, 8])
+def test_matvec_rows_matches_oracle(backend, encoding, rows, columns, tokens):
+    import torch
+    w = quantized(encoding, rows, columns, 9)
+    in_stride, out_stride = columns + 64, rows + 8
+    x = np.zeros((tokens, in_stride), np.float32)
+    x[:, :columns] = gaussian(10 + tokens, (tokens, columns))
+    out = torch.full((tokens, out_stride), np.nan, dtype=torch.float32, device="cuda")
+    backend.matvec_rows(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), in_stride, out, out_stride, tokens)
+    backend.sync()
+    xs = x[:, :columns]
+    want = orc.matmul(encoding, rows, columns, w, xs)
+    check_close(out.cpu().numpy()[:, :rows], want, mass(encoding, w, rows, columns, xs), F32_K, "rows")
+
+
+# ---------------------------------------------------------------- MFMA tile
+TILE_CASES = [
+    (12, 512, 5120, 8), (14, 512, 5120, 8), (8, 512, 4096, 8),
+    (12, 256, 1280, 37), (14, 256, 1280, 20), (8, 256, 1280, 5),
+    (12, 1024, 5120, 130), (14, 520, 17408, 64), (12, 136, 17408, 200),
+]
+
+
+@pytest.mark.parametrize("xdtype", ["f16", "f32"])
+@pytest.mark.parametrize("encoding,rows,columns,tokens", TILE_CASES)
+def test_tile_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
+    import torch
+    w = quantized(encoding, rows, columns, 20 + tokens)
+    x32 = gaussian(30 + tokens, (tokens, columns))
+    if xdtype == "f16":
+        x16 = x32.astype(np.float16)
+        xg = to_gpu(x16)
+        xref = x16.astype(np.float32)
+        k = F16_K / 2   # only the weights are rounded
+    else:
+        xg = to_gpu(x32)
+        xref = x32
+        k = F16_K
+    out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_TILE, nq.Matrix(encoding, rows, columns, to_gpu(w)), xg, columns, out, rows, tokens)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, xref)
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, "tile")
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_tile_tamed_fixture_blocks(backend, encoding):
+    """metal-check.zig:4355-4436: fixture blocks with tamed scales, 40 rows,
+    token counts 37/20/16/9/8/5/1, against the oracle."""
+    import torch
+    rows, columns = 40, 256 if encoding != 8 else 64
+    w = tame(tiled(encoding, rows, columns), encoding)
+    mw = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    for tokens in (37, 20, 16, 9, 8, 5, 1):
+        x = gaussian(tokens, (tokens, columns))
+        out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+        backend.matmul_kernel(nq.KERNEL_TILE, mw, to_gpu(x), columns, out, rows, tokens)
+        backend.sync()
+        want = orc.matmul(encoding, rows, columns, w, x)
+        check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x), F16_K, f"tamed {tokens}")
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 8, 64])
+def test_matmul_routing_matches_oracle(backend, tokens):
+    import torch
+    rows, columns = 256, 5120
+    w = quantized(12, rows, columns, 5)
+    x = gaussian(6, (tokens, columns))
+    out = torch.empty((tokens, rows), dtype=torch.float32, device="cuda")
+    backend.matmul(nq.Matrix(12, rows, columns, to_gpu(w)), to_gpu(x), columns, out, rows, tokens)
+    backend.sync()
+    want = orc.matmul(12, rows, columns, w, x)
+    check_close(out.cpu().numpy(), want, mass(12, w, rows, columns, x), F16_K, "matmul")
+
+
+def test_matmul_refusals(backend):
+    import torch
+    w = to_gpu(quantized(12, 16, 256, 1))
+    x = torch.zeros((4, 256), device="cuda")
+    out = torch.zeros((4, 16), device="cuda")
+    with pytest.raises(nq.InvalidShape):   # rows % 8
+        backend.matmul(nq.Matrix(12, 12, 256, w[: 12 * 144]), x, 256, out, 16, 4)
+    with pytest.raises(nq.InvalidShape):   # tokens 0
+        backend.matmul(nq.Matrix(12, 16, 256, w), x, 256, out, 16, 0)
+    with pytest.raises(nq.InvalidShape):   # in_stride < columns
+        backend.matmul(nq.Matrix(12, 16, 256, w), x, 128, out, 16, 4)
+    with pytest.raises(nq.InvalidShape):   # rows tile kernel limit
+        backend.matmul_kernel(nq.KERNEL_ROWS, nq.Matrix(12, 16, 256, w), x, 256, out, 16, 9)
+
+
+# ---------------------------------------------------------------- segments / argmax
+def test_segments_plain_and_silu_pair(backend):
+    import torch
+    columns = 5120
+    shapes = [(12, 1024), (12, 512), (14, 256), (8, 128)]
+    ws = [quantized(e, r, columns, 40 + i) for i, (e, r) in enumerate(shapes)]
+    x = gaussian(41, columns)
+    xg = to_gpu(x)
+    outs = [torch.full((r,), np.nan, device="cuda") for _, r in shapes]
+    segs = [(nq.Matrix(e, r, columns, to_gpu(w)), o) for (e, r), w, o in zip(shapes, ws, outs)]
+    backend.matvec_segments(segs, xg, nq.SEGMENT_PLAIN)
+    backend.sync()
+    for (e, r), w, o in zip(shapes, ws, outs):
+        check_close(o.cpu().numpy(), orc.matvec(e, r, columns, w, x), mass(e, w, r, columns, x)[0], F32_K, "segment")
+    # gate/up pair: out = silu(gate x) * (up x)
+    gate, up = quantized(12, 1024, columns, 50), quantized(12, 1024, columns, 51)
+    pair_out = torch.full((1024,), np.nan, device="cuda")
+    backend.matvec_segments([(nq.Matrix(12, 1024, columns, to_gpu(gate)), pair_out),
+                             (nq.Matrix(12, 1024, columns, to_gpu(up)), pair_out)], xg, nq.SEGMENT_SILU_MUL_PAIR)
+    backend.sync()
+    g = orc.matvec(12, 1024, columns, gate, x).astype(np.float64)
+    u = orc.matvec(12, 1024, columns, up, x).astype(np.float64)
+    want = g / (1 + np.exp(-g)) * u
+    got = pair_out.cpu().numpy()
+    mg, mu = mass(12, gate, 1024, columns, x)[0], mass(12, up, 1024, columns, x)[0]
+    # first-order propagation of the two F32 bounds through silu(g)*u (|silu'| <= 1.1)
+    bound = 1.1 * np.abs(u) * (F32_K * mg + 1e-6) + np.abs(g) * (F32_K * mu + 1e-6) + 1e-6
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def test_argmax_first_maximum(backend):
+    import torch
+    v = gaussian(60, 151936)
+    v[77777] = 50.0
+    v[99999] = 50.0
+    assert backend.argmax(to_gpu(v)) == orc.argmax(v) == 77777
+    v[5] = np.inf
+    with pytest.raises(nq.NonFiniteResult):
+        backend.argmax(to_gpu(v))
+    assert backend.argmax(torch.tensor([3.0], device="cuda")) == 0

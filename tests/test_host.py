@@ -1,0 +1,88 @@
+"""CPU-side checks of libnuq.so: it loads, exports every symbol include/nuq.h
+declares, validates rows as decode.validateRow does, and its host quantizers
+write blocks the oracle decodes (Q8_0 bit-identical to the reference encoder).
+No compute is launched: this file runs without a GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import nuclis_amd as nq
+from nuclis_amd.synth import gaussian
+from oracle import oracle as orc
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "nuq.h").read_text()
+    return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(nuq_\w+)\(", text, re.M)))
+
+
+def test_header_and_python_binding_agree():
+    assert declared_functions() == sorted(nq.backend.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(nq.backend.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_validate_row_matches_oracle(encoding):
+    n, size = nq.LAYOUT[encoding]
+    cases = [(0, 0), (size, n), (size - 1, n), (size + 1, n), (size, 2 * n), (2 * size, n), (size, n - 1),
+             (3 * size, 3 * n), (size, n + 1)]
+    for byte_count, elements in cases:
+        try:
+            orc.validate_row(encoding, byte_count, elements)
+            want = None
+        except orc.OracleError as e:
+            want = e.name
+        try:
+            nq.validate_row(encoding, byte_count, elements)
+            got = None
+        except nq.NuqError as e:
+            got = type(e).__name__
+        assert got == want, (byte_count, elements)
+    with pytest.raises(nq.UnsupportedTensorEncoding):
+        nq.validate_row(999, 1, 1)
+
+
+def test_q8_0_quantizer_is_the_reference_encoder():
+    w = gaussian(0, (64, 4096), 0.02)
+    w[0, :32] = 0
+    w[1, :32] *= 1e6
+    w[2, 5] = np.nan
+    got = nq.quantize(8, w)
+    for r in range(w.shape[0]):
+        assert np.array_equal(got[r], orc.q8_0_row(w[r])), r
+
+
+@pytest.mark.parametrize("encoding,tol", [(12, 0.6), (14, 0.55)])
+def test_k_quantizers_round_trip(encoding, tol):
+    """Own Q4_K/Q6_K quantizers: decode(quantize(w)) is within `tol` of the
+    group's quantization step of w (their bytes are unpinned by design; parity
+    of whatever bytes they write is checked by decoding them)."""
+    w = gaussian(3, (16, 1024), 0.02)
+    q = nq.quantize(encoding, w)
+    assert q.shape == (16, nq.row_bytes(encoding, 1024))
+    back = orc.decode_matrix(encoding, q, 16, 1024)
+    err = np.abs(back - w)
+    group = 32 if encoding == 12 else 16
+    spread = w.reshape(16, -1, group)
+    step = (spread.max(-1) - np.minimum(spread.min(-1), 0)) / 15 if encoding == 12 else np.abs(spread).max(-1) / 31
+    # scale quantization (6 or 8 bits) widens the step by a few percent
+    assert np.all(err.reshape(16, -1, group) <= step[..., None] * tol + 1e-7)
+    rel = np.linalg.norm(back - w) / np.linalg.norm(w)
+    assert rel < (0.1 if encoding == 12 else 0.03)
+
+
+def test_quantizer_refusals():
+    with pytest.raises(nq.InvalidRowLength):
+        nq.quantize(12, np.zeros((2, 100), np.float32))
+    with pytest.raises(nq.UnsupportedTensorEncoding):
+        nq.quantize(3, np.zeros((2, 256), np.float32))
