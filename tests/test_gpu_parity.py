@@ -279,7 +279,7 @@ def test_matmul_routing_matches_oracle(backend, tokens):
 
 def test_matmul_refusals(backend):
     import torch
-    w = to_gpu(quantized(12, 16, 256, 1))
+    w = to_gpu(quantized(12, 16, 256, 1).ravel())
     x = torch.zeros((4, 256), device="cuda")
     out = torch.zeros((4, 16), device="cuda")
     with pytest.raises(nq.InvalidShape):   # rows % 8
