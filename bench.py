@@ -194,11 +194,12 @@ def main():
         extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
                                                              args.steps, args.warmup).items()
                                if k not in ("w", "x", "y0")}
-        extras["prefill_q6k_down_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q6_K, 5120, 17408, 4096)
-        extras["prefill_q4k_gate_m512"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 512)
-        for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
-            extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 8,
-                                                               reps=200, warmup=20, kernel=kid)
+        if not only or "prefill" in only:
+            extras["prefill_q6k_down_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q6_K, 5120, 17408, 4096)
+            extras["prefill_q4k_gate_m512"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 512)
+            for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
+                extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120,
+                                                                   8, reps=200, warmup=20, kernel=kid)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(g["w"], x_host, rows, columns, args.cpu_seconds)

@@ -14,6 +14,7 @@
 // and a 16-byte aligned input; anything else runs the generic control.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -99,6 +100,21 @@ int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
     return rows >= 8192 ? 4 : 2;
 }
 
+// The decode GEMV: Q4_K on the integer-dot K-split kernel, the other
+// encodings on the row-per-wave kernels.
+int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, float *out) {
+    if (m->encoding == NUQ_Q4_K) {
+        const int config = 0;  // R=2 rows per quarter-wave, one 15-wave workgroup per CU
+        hipError_t e = nuq::launch_gemv_q4k_int(ctx->stream, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                                (uint32_t)m->columns, x, out, config);
+        if (e != hipErrorInvalidValue) return hip_check(ctx, e, "q4_k gemv launch");
+    }
+    return hip_check(ctx,
+                     nuq::launch_gemv(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                      (uint32_t)m->columns, x, out, gemv_rows_per_wave(m->encoding, m->rows)),
+                     "gemv launch");
+}
+
 int run_generic(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const void *x, uint32_t x_f16,
                 uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
     return hip_check(ctx,
@@ -131,13 +147,7 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
     if (ctx->generic_only || kernel == NUQ_KERNEL_GENERIC || !aligned)
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_AUTO) {
-        if (tokens == 1 && !f16) {
-            return hip_check(ctx,
-                             nuq::launch_gemv(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
-                                              (uint32_t)m->rows, (uint32_t)m->columns, (const float *)x, out,
-                                              gemv_rows_per_wave(m->encoding, m->rows)),
-                             "gemv launch");
-        }
+        if (tokens == 1 && !f16) return run_gemv(ctx, m, stride, (const float *)x, out);
         kernel = tokens <= 3 ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
     }
     if (kernel == NUQ_KERNEL_ROWS)
@@ -257,10 +267,7 @@ int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out
         return fail(ctx, NUQ_INVALID_SHAPE, "input and output must be 4-byte aligned");
     if (ctx->generic_only || !vector_aligned(m, stride, x))
         return run_generic(ctx, m, stride, x, 0, m->columns, out, m->rows, 1);
-    return hip_check(ctx,
-                     nuq::launch_gemv(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
-                                      (uint32_t)m->columns, x, out, gemv_rows_per_wave(m->encoding, m->rows)),
-                     "gemv launch");
+    return run_gemv(ctx, m, stride, x, out);
 }
 
 int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint64_t in_stride, float *out,

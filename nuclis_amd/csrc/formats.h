@@ -125,6 +125,16 @@ __device__ __forceinline__ float decode_value(uint32_t encoding, const uint8_t *
 template <int E>
 __device__ __forceinline__ float ubyte_f(uint32_t w) { return (float)((w >> (8 * E)) & 0xffu); }
 
+// a & M through an instruction the compiler cannot see into, so the
+// following byte extractions select v_cvt_f32_ubyteN on the masked word
+// instead of re-deriving each nibble with v_bfe_u32.
+template <uint32_t M>
+__device__ __forceinline__ uint32_t opaque_and(uint32_t a) {
+    uint32_t r;
+    asm("v_and_b32_e32 %0, %2, %1" : "=v"(r) : "v"(a), "n"(M));
+    return r;
+}
+
 // Unaligned 32-bit load. gfx9 global memory runs in unaligned access mode
 // under ROCm, so a dword load at a 2-byte aligned address returns the four
 // bytes at that address.

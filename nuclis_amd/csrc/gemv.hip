@@ -50,26 +50,51 @@ __global__ void __launch_bounds__(256) dequant_rows_kernel(uint32_t encoding, co
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K lane work: one 16-byte qs chunk of one block against the lane's x.
-struct Q4kLane {
-    float xa[16], xb[16];
-    float sxa, sxb;
-    uint32_t j;  // qs pair index: groups 2j and 2j+1
+// Q4_K. A half-wave (32 lanes) covers 4 consecutive blocks of R rows: lane
+// (slot, c) holds 16-byte qs chunk c of block slot, i.e. columns 16*(c&1)..+16
+// of groups 2j and 2j+1 (j = c>>1), whose low / high nibbles share the bytes.
+// The two half-waves of a wave take different rows and the same columns, so
+// every block count that is a multiple of 4 (20, 24, 68 at the configs)
+// keeps all lanes busy. High nibbles are converted in place (x16) and the
+// 1/16 folded into their scale, so each value costs one v_cvt_f32_ubyteN and
+// one FMA.
+
+// Pair (sa, ma, sb, mb) of six-bit scales/minima for groups 2j, 2j+1 without
+// branches (lanes of one wave take both forms): quant/decode.zig:155-158.
+struct PairShift {
+    uint32_t shift;
+    bool direct;
 };
 
-__device__ __forceinline__ float q4k_chunk_dot(const uint4 hdr, const uint4 qs, const float *xa, const float *xb,
-                                               float sxa, float sxb, uint32_t j) {
-    float d = half_bits(hdr.x & 0xffffu);
-    float dmin = half_bits(hdr.x >> 16);
-    uint32_t sc0, m0, sc1, m1;
-    q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, &sc0, &m0);
-    q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
-    float lo = 0.f, hi = 0.f;
+__device__ __forceinline__ void q4k_pair(uint32_t s0, uint32_t s1, uint32_t s2, PairShift ps, float *sa, float *ma,
+                                         float *sb, float *mb) {
+    const uint32_t x = s0 >> ps.shift, y = s1 >> ps.shift, z = s2 >> ps.shift;
+    const uint32_t a = ps.direct ? (x & 63u) : ((z & 15u) | (((x >> 6) & 3u) << 4));
+    const uint32_t m = ps.direct ? (y & 63u) : (((z >> 4) & 15u) | (((y >> 6) & 3u) << 4));
+    const uint32_t b = ps.direct ? ((x >> 8) & 63u) : (((z >> 8) & 15u) | (((x >> 14) & 3u) << 4));
+    const uint32_t n = ps.direct ? ((y >> 8) & 63u) : (((z >> 12) & 15u) | (((y >> 14) & 3u) << 4));
+    *sa = (float)a;
+    *ma = (float)m;
+    *sb = (float)b;
+    *mb = (float)n;
+}
+
+__device__ __forceinline__ PairShift pair_shift(uint32_t j) {
+    PairShift p;
+    p.direct = j < 2;
+    p.shift = p.direct ? 16 * j : 16 * j - 32;
+    return p;
+}
+
+// Low nibbles against xa, high nibbles (kept at x16) against xb.
+__device__ __forceinline__ void q4k_dot16(const uint4 qs, const float *xa, const float *xb, float *lo_out,
+                                          float *hi_out) {
     const uint32_t words[4] = {qs.x, qs.y, qs.z, qs.w};
+    float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        uint32_t l4 = words[k] & 0x0f0f0f0fu;
-        uint32_t h4 = (words[k] >> 4) & 0x0f0f0f0fu;
+        const uint32_t l4 = opaque_and<0x0f0f0f0fu>(words[k]);
+        const uint32_t h4 = opaque_and<0xf0f0f0f0u>(words[k]);
         lo = fmaf(ubyte_f<0>(l4), xa[4 * k + 0], lo);
         lo = fmaf(ubyte_f<1>(l4), xa[4 * k + 1], lo);
         lo = fmaf(ubyte_f<2>(l4), xa[4 * k + 2], lo);
@@ -79,8 +104,26 @@ __device__ __forceinline__ float q4k_chunk_dot(const uint4 hdr, const uint4 qs, 
         hi = fmaf(ubyte_f<2>(h4), xb[4 * k + 2], hi);
         hi = fmaf(ubyte_f<3>(h4), xb[4 * k + 3], hi);
     }
-    float r = (d * (float)sc0) * lo + (d * (float)sc1) * hi;
-    return r - (dmin * (float)m0) * sxa - (dmin * (float)m1) * sxb;
+    *lo_out = lo;
+    *hi_out = hi;
+}
+
+__device__ __forceinline__ float q4k_chunk_dot(const uint4 hdr, const uint4 qs, const float *xa, const float *xb,
+                                               float sxa, float sxb, PairShift ps) {
+    float d = half_bits(hdr.x & 0xffffu);
+    float dmin = half_bits(hdr.x >> 16);
+    float sa, ma, sb, mb;
+    q4k_pair(hdr.y, hdr.z, hdr.w, ps, &sa, &ma, &sb, &mb);
+    float lo, hi;
+    q4k_dot16(qs, xa, xb, &lo, &hi);
+    float r = (d * sa) * lo + (d * sb * 0.0625f) * hi;
+    return r - dmin * (ma * sxa + mb * sxb);
+}
+
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+    for (int offset = 16; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
 }
 
 template <int R>
@@ -89,25 +132,25 @@ __global__ void __launch_bounds__(256) gemv_q4k_kernel(const uint8_t *__restrict
                                                         float *__restrict__ y) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t row0 = wave * R;
-    if (row0 >= rows) return;
-    const uint32_t c = lane & 7, slot = lane >> 3;
+    if (wave * 2 * R >= rows) return;
+    const uint32_t rg = lane >> 5, slot = (lane >> 3) & 3, c = lane & 7;
     const uint32_t j = c >> 1, half16 = (c & 1) * 16;
-    const uint8_t *rowp[R];
+    const uint32_t row0 = wave * 2 * R + rg * R;
+    const PairShift ps = pair_shift(j);
+    const uint8_t *hp[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rowp[r] = w + (uint64_t)min(row0 + r, rows - 1) * stride;
+    for (int r = 0; r < R; ++r) hp[r] = w + (uint64_t)min(row0 + r, rows - 1) * stride + slot * 144;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
 
-    for (uint32_t b = slot; b < nblocks; b += 8) {
-        uint4 hdr[R], qs[R];
+    uint4 hdr[R], qs[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *blk = rowp[r] + (uint64_t)b * 144;
-            hdr[r] = *(const uint4 *)blk;
-            qs[r] = *(const uint4 *)(blk + 16 + c * 16);
-        }
+    for (int r = 0; r < R; ++r) {
+        hdr[r] = *(const uint4 *)hp[r];
+        qs[r] = *(const uint4 *)(hp[r] + 16 + c * 16);
+    }
+    for (uint32_t b = slot; b < nblocks; b += 4) {
         const float *xp = x + b * 256 + j * 64 + half16;
         float xa[16], xb[16];
 #pragma unroll
@@ -117,19 +160,35 @@ __global__ void __launch_bounds__(256) gemv_q4k_kernel(const uint8_t *__restrict
             xa[4 * k] = a.x; xa[4 * k + 1] = a.y; xa[4 * k + 2] = a.z; xa[4 * k + 3] = a.w;
             xb[4 * k] = bb.x; xb[4 * k + 1] = bb.y; xb[4 * k + 2] = bb.z; xb[4 * k + 3] = bb.w;
         }
-        float sxa = 0.f, sxb = 0.f;
+        // prefetch the next block of every row before computing this one
+        uint4 nhdr[R], nqs[R];
+        const bool more = b + 4 < nblocks;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            sxa += xa[k];
-            sxb += xb[k];
+        for (int r = 0; r < R; ++r) {
+            hp[r] += 4 * 144;
+            if (more) {
+                nhdr[r] = *(const uint4 *)hp[r];
+                nqs[r] = *(const uint4 *)(hp[r] + 16 + c * 16);
+            }
         }
+        float sxa = ((xa[0] + xa[1]) + (xa[2] + xa[3])) + ((xa[4] + xa[5]) + (xa[6] + xa[7])) +
+                    (((xa[8] + xa[9]) + (xa[10] + xa[11])) + ((xa[12] + xa[13]) + (xa[14] + xa[15])));
+        float sxb = ((xb[0] + xb[1]) + (xb[2] + xb[3])) + ((xb[4] + xb[5]) + (xb[6] + xb[7])) +
+                    (((xb[8] + xb[9]) + (xb[10] + xb[11])) + ((xb[12] + xb[13]) + (xb[14] + xb[15])));
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += q4k_chunk_dot(hdr[r], qs[r], xa, xb, sxa, sxb, j);
+        for (int r = 0; r < R; ++r) acc[r] += q4k_chunk_dot(hdr[r], qs[r], xa, xb, sxa, sxb, ps);
+        if (more) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                hdr[r] = nhdr[r];
+                qs[r] = nqs[r];
+            }
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float v = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < rows) y[row0 + r] = v;
+        float v = half_wave_sum(acc[r]);
+        if ((lane & 31) == 0 && row0 + r < rows) y[row0 + r] = v;
     }
 }
 
@@ -511,7 +570,7 @@ __device__ __forceinline__ void gemv_rows_any(uint32_t encoding, const uint8_t *
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint8_t *blk = rowp[r] + (uint64_t)b * 144;
-                acc[r] += q4k_chunk_dot(*(const uint4 *)blk, *(const uint4 *)(blk + 16 + c * 16), xa, xb, sxa, sxb, j);
+                acc[r] += q4k_chunk_dot(*(const uint4 *)blk, *(const uint4 *)(blk + 16 + c * 16), xa, xb, sxa, sxb, pair_shift(j));
             }
         }
     } else if (encoding == 14) {
@@ -596,7 +655,7 @@ hipError_t launch_dequant_rows(hipStream_t s, uint32_t encoding, const uint8_t *
 template <int R>
 static hipError_t launch_gemv_r(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                                 uint32_t nblocks, const float *x, float *y) {
-    uint32_t waves = div_up(rows, R);
+    uint32_t waves = div_up(rows, encoding == 12 ? 2 * R : R);
     dim3 grid(div_up(waves, 4)), block(256);
     switch (encoding) {
     case 12: hipLaunchKernelGGL(gemv_q4k_kernel<R>, grid, block, 0, s, w, stride, rows, nblocks, x, y); break;

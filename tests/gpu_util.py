@@ -6,6 +6,9 @@ Tolerances (stated where they are used):
     |gpu - ref| <= 4e-6 * sum|w*x| + 1e-6 per output, the reference's bound
     for its matvecs (metal-check.zig:3976), and normwise
     max|gpu - ref| / max|ref| <= 2e-3 (the stated max relative error);
+  * integer-dot GEMV (activations rounded to 16 bits of their 32-value
+    slice maximum before the exact integer dot): the F32 bound plus the
+    rigorous rounding term sum_c |w[r,c]| * max|x slice(c)| / 65278;
   * f16 MFMA tile: weights (and F32 activations) are rounded to f16, each
     term then carries at most 2^-11 relative error per rounded operand, so
     |gpu - ref| <= 2e-3 * sum|w*x| + 1e-6 per output, plus the same 2e-3
@@ -30,13 +33,21 @@ def mass(encoding, w_bytes, rows, columns, x):
     return np.abs(np.atleast_2d(x).astype(np.float64)) @ np.abs(dec).T
 
 
-def check_close(got, want, mass_, k, label=""):
+def xq_mass(encoding, w_bytes, rows, columns, x):
+    """sum_c |w[r,c]| * max|x over c's 32-column slice| / 65278 (F64)."""
+    dec = orc.decode_matrix(encoding, w_bytes, rows, columns).astype(np.float64)
+    xs = np.atleast_2d(x).astype(np.float64)
+    amax = np.repeat(np.abs(xs).reshape(xs.shape[0], -1, 32).max(-1), 32, axis=1)
+    return (amax / 65278.0) @ np.abs(dec).T
+
+
+def check_close(got, want, mass_, k, label="", extra=0.0):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     assert got.shape == want.shape, (got.shape, want.shape)
     assert np.all(np.isfinite(got)), f"{label}: non-finite output"
     err = np.abs(got - want)
-    bound = k * mass_ + 1e-6
+    bound = k * mass_ + extra + 1e-6
     worst = np.unravel_index(np.argmax(err - bound), err.shape)
     assert np.all(err <= bound), (f"{label}: |d|={err[worst]:.3e} > bound {bound[worst]:.3e} at {worst} "
                                   f"(got {got[worst]}, want {want[worst]})")

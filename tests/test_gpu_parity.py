@@ -13,12 +13,13 @@ import pytest
 import nuclis_amd as nq
 from nuclis_amd.synth import gaussian
 from oracle import oracle as orc
-from tests.gpu_util import check_close, mass, to_gpu
+from tests.gpu_util import check_close, mass, to_gpu, xq_mass
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "decoder_fixtures.json").read_text())
 F32_K = 4e-6   # reference matvec bound (metal-check.zig:3976)
+INT_GEMV = {12}  # encodings whose M=1 GEMV runs on the integer-dot kernel
 F16_K = 2e-3   # f16-rounded operands
 
 
@@ -128,7 +129,8 @@ def test_matvec_matches_oracle(backend, encoding, rows, columns):
     backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
     backend.sync()
     want = orc.matvec(encoding, rows, columns, w, x)
-    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"matvec {encoding}")
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"matvec {encoding}",
+                extra=xq_mass(encoding, w, rows, columns, x)[0] if encoding in INT_GEMV else 0.0)
 
 
 @pytest.mark.parametrize("encoding", [8, 12, 14])
@@ -145,7 +147,7 @@ def test_matvec_tiled_fixture_blocks_and_basis_columns(backend, encoding):
     backend.matvec(m, to_gpu(x), out)
     backend.sync()
     check_close(out.cpu().numpy(), orc.matvec(encoding, rows, columns, w, x), mass(encoding, w, rows, columns, x)[0],
-                F32_K, "tiled")
+                F32_K, "tiled", extra=xq_mass(encoding, w, rows, columns, x)[0] if encoding in INT_GEMV else 0.0)
     dec = orc.decode_matrix(encoding, w, rows, columns)
     for column in (0, columns // 2 + 1, columns - 1):
         e = np.zeros(columns, np.float32)
