@@ -182,6 +182,320 @@ __global__ void __launch_bounds__(256) tile_kernel(const uint8_t *__restrict__ w
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill tile: BM x BN = 256 tokens x 256 weight rows, 512 threads as 2 x 4
+// waves of 128 x 64 (4 x 2 MFMA 32x32 blocks, 128 F32 accumulators a lane).
+// LDS holds two K slabs (double buffer): while the MFMAs of slab k run, the
+// raw GGUF bytes and activations of slab k+1 are in flight in registers;
+// they are dequantised into the other buffer after the MFMAs, so there is
+// one barrier per slab.
+//
+// Workgroup order: the hardware deals workgroups to the 8 XCDs round-robin,
+// each XCD with its own L2. The linear id is first regrouped so that every
+// XCD owns a contiguous range of tiles, then walked GROUP_M tiles down the
+// token axis before moving across rows, so the ~32 workgroups resident on
+// one XCD share a few activation panels and weight panels in its L2.
+template <typename XT>
+struct XLoad;
+template <>
+struct XLoad<_Float16> {
+    half8 v[4];
+    __device__ __forceinline__ void load(const _Float16 *p, bool valid) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (valid) v[k] = ((const half8 *)p)[k];
+            else
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[k][e] = (_Float16)0.f;
+        }
+    }
+    __device__ __forceinline__ void store(_Float16 *dst, uint32_t c) const { *(half8 *)(dst + 8 * c) = v[c]; }
+};
+template <>
+struct XLoad<float> {
+    float4 v[8];
+    __device__ __forceinline__ void load(const float *p, bool valid) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = valid ? ((const float4 *)p)[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __device__ __forceinline__ void store(_Float16 *dst, uint32_t k) const {
+        half8 h;
+        h[0] = (_Float16)v[2 * k].x; h[1] = (_Float16)v[2 * k].y; h[2] = (_Float16)v[2 * k].z; h[3] = (_Float16)v[2 * k].w;
+        h[4] = (_Float16)v[2 * k + 1].x; h[5] = (_Float16)v[2 * k + 1].y; h[6] = (_Float16)v[2 * k + 1].z; h[7] = (_Float16)v[2 * k + 1].w;
+        *(half8 *)(dst + 8 * k) = h;
+    }
+};
+
+// Raw bytes of the 32 weight values a thread owns in one K slab, kept in
+// registers between the global load and the dequantisation. `dequant(c)`
+// writes chunk c (0..3) of the 32 values, so the work can be spread between
+// the MFMA sub-steps. Values are (d*sc)*q - dmin*m (Q4_K), (d*sc)*(q-32)
+// (Q6_K) and d*q (Q8_0) in F32 with one FMA, then rounded to f16; the
+// decoders' separate rounding of the product is not kept here (the tile
+// rounds every weight to f16 anyway).
+template <uint32_t ENC>
+struct WRaw;
+template <>
+struct WRaw<12> {
+    uint4 hdr, qs;
+    float mul0, off0, mul1, off1;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 144;
+        hdr = *(const uint4 *)blk;
+        qs = *(const uint4 *)(blk + 16 + (ks & 3) * 32 + part * 16);
+    }
+    __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
+        if (c == 0) {
+            const uint32_t p = ks & 3;
+            const float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scale_min(2 * p, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+            q4k_scale_min(2 * p + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+            mul0 = d * (float)sc0;
+            off0 = dmin * (float)m0;
+            mul1 = d * (float)sc1 * 0.0625f;  // high nibbles are converted in place (x16)
+            off1 = dmin * (float)m1;
+        }
+        const uint32_t word = c == 0 ? qs.x : c == 1 ? qs.y : c == 2 ? qs.z : qs.w;
+        const uint32_t lo = opaque_and<0x0f0f0f0fu>(word), hi = opaque_and<0xf0f0f0f0u>(word);
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        half4 l, h;
+        l[0] = (_Float16)fmaf(mul0, ubyte_f<0>(lo), -off0);
+        l[1] = (_Float16)fmaf(mul0, ubyte_f<1>(lo), -off0);
+        l[2] = (_Float16)fmaf(mul0, ubyte_f<2>(lo), -off0);
+        l[3] = (_Float16)fmaf(mul0, ubyte_f<3>(lo), -off0);
+        h[0] = (_Float16)fmaf(mul1, ubyte_f<0>(hi), -off1);
+        h[1] = (_Float16)fmaf(mul1, ubyte_f<1>(hi), -off1);
+        h[2] = (_Float16)fmaf(mul1, ubyte_f<2>(hi), -off1);
+        h[3] = (_Float16)fmaf(mul1, ubyte_f<3>(hi), -off1);
+        *(half4 *)(out + part * 16 + 4 * c) = l;
+        *(half4 *)(out + 32 + part * 16 + 4 * c) = h;
+    }
+};
+template <>
+struct WRaw<14> {
+    uint32_t ql[8], qh[8];
+    uint32_t sc;  // the two int8 scales of this quarter (bytes 0, 1)
+    uint32_t d16;
+    float mul_a, mul_b;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 210;
+        const uint32_t h = (ks & 3) >> 1, q = 2 * (ks & 1) + part;
+        const uint8_t *lp = blk + h * 64 + (q & 1) * 32;
+        const uint8_t *hp = blk + 128 + h * 32;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            ql[k] = load_u32_unaligned(lp + 4 * k);
+            qh[k] = load_u32_unaligned(hp + 4 * k);
+        }
+        sc = load_u16_bytes(blk + 192 + h * 8 + 2 * q);
+        d16 = load_u16_bytes(blk + 208);
+    }
+    __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
+        const uint32_t q = 2 * (ks & 1) + part;
+        const uint32_t lshift = (q >> 1) * 4, hshift = 2 * q;
+        if (c == 0) {
+            const float d = half_bits(d16);
+            mul_a = d * (float)(int8_t)(sc & 0xff);
+            mul_b = d * (float)(int8_t)(sc >> 8);
+        }
+        const float mul = c < 2 ? mul_a : mul_b;
+        half8 v;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint32_t u = opaque_and<0x0f0f0f0fu>(ql[2 * c + kk] >> lshift) |
+                               opaque_and<0x30303030u>((qh[2 * c + kk] >> hshift) << 4);
+            v[kk * 4 + 0] = (_Float16)fmaf(mul, ubyte_f<0>(u), -32.f * mul);
+            v[kk * 4 + 1] = (_Float16)fmaf(mul, ubyte_f<1>(u), -32.f * mul);
+            v[kk * 4 + 2] = (_Float16)fmaf(mul, ubyte_f<2>(u), -32.f * mul);
+            v[kk * 4 + 3] = (_Float16)fmaf(mul, ubyte_f<3>(u), -32.f * mul);
+        }
+        *(half8 *)(out + part * 32 + 8 * c) = v;
+    }
+};
+template <>
+struct WRaw<8> {
+    uint32_t q[8];
+    uint32_t d16;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(2 * ks + part) * 34;
+        d16 = load_u16_bytes(blk);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = load_u32_unaligned(blk + 2 + 4 * k);
+    }
+    __device__ __forceinline__ void dequant(uint32_t, uint32_t part, uint32_t c, _Float16 *out) {
+        const float d = half_bits(d16);
+        half8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (_Float16)(d * (float)(int8_t)((q[2 * c + e / 4] >> (8 * (e & 3))) & 0xff));
+        *(half8 *)(out + part * 32 + 8 * c) = v;
+    }
+};
+
+constexpr int PF_BM = 256, PF_BN = 256, PF_THREADS = 512, PF_GROUP_M = 4;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// f16 activations go global -> LDS without registers (global_load_lds_dwordx4):
+// lane i of wave instruction q fills 16-byte slot 64q + i of the padded
+// tile (9 slots a row: 8 of data, 1 of padding, so rows keep the 144-byte
+// pitch the fragment reads want). Padding slots load a valid address and
+// are never read. Rows past `tokens` re-read the last token: their outputs
+// are never stored.
+__device__ __forceinline__ void x_dma(const _Float16 *__restrict__ x, uint64_t in_stride, uint32_t m_base,
+                                      uint32_t tokens, uint32_t k0, _Float16 *lds_tile, uint32_t wave,
+                                      uint32_t lane) {
+    constexpr uint32_t SLOTS = PF_BM * 9, INSTRS = SLOTS / 64;  // 36
+    for (uint32_t q = wave; q < INSTRS; q += PF_THREADS / 64) {
+        const uint32_t slot = 64 * q + lane;
+        const uint32_t row = slot / 9, chunk = slot % 9;
+        const uint32_t tok = min(m_base + row, tokens - 1);
+        const _Float16 *src = x + (uint64_t)tok * in_stride + k0 + 8 * (chunk == 8 ? 0 : chunk);
+        __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(lds_tile + 64 * q * 8), 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void tile_coords(uint32_t id, uint32_t tm, uint32_t tn, uint32_t *pid_m, uint32_t *pid_n) {
+    const uint32_t total = tm * tn;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;  // contiguous range per XCD
+    const uint32_t per_group = PF_GROUP_M * tn;
+    const uint32_t group = id / per_group;
+    const uint32_t first_m = group * PF_GROUP_M;
+    const uint32_t gm = min(tm - first_m, (uint32_t)PF_GROUP_M);
+    const uint32_t in_group = id % per_group;
+    *pid_m = first_m + in_group % gm;
+    *pid_n = in_group / gm;
+}
+
+template <uint32_t ENC, typename XT>
+__global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+                                                              uint32_t rows, uint32_t columns,
+                                                              const XT *__restrict__ x, uint64_t in_stride,
+                                                              float *__restrict__ y, uint64_t out_stride,
+                                                              uint32_t tokens) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_smem[];
+    // buffer b: activations at pf_smem + b*XS, weights at pf_smem + 2*XS + b*WS
+    constexpr uint32_t XS = PF_BM * LDS_PITCH, WS = PF_BN * LDS_PITCH;
+
+    const uint32_t tm = (tokens + PF_BM - 1) / PF_BM, tn = (rows + PF_BN - 1) / PF_BN;
+    uint32_t pid_m, pid_n;
+    tile_coords(blockIdx.x, tm, tn, &pid_m, &pid_n);
+    const uint32_t m_base = pid_m * PF_BM, n_base = pid_n * PF_BN;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 128 x 64
+    const uint32_t srow = tid >> 1, part = tid & 1;
+    const uint8_t *wrow = w + (uint64_t)min(n_base + srow, rows - 1) * stride;
+    const uint32_t xtok = m_base + srow;
+    const bool xvalid = xtok < tokens;
+    const XT *xrow = x + (uint64_t)(xvalid ? xtok : 0) * in_stride + part * 32;
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // Pipeline. Activations: slab ks+1 is copied global -> LDS during step
+    // ks (f16 input; F32 input is converted through registers after the
+    // MFMAs). Weights: two register sets hold the raw GGUF bytes of slabs
+    // ks+1 and ks+2; slab ks+1 is dequantised chunk by chunk between the
+    // MFMA sub-steps of slab ks (so one wave keeps both the matrix core and
+    // the VALU busy), while slab ks+2 is in flight.
+    constexpr bool DMA = sizeof(XT) == 2;
+    XLoad<XT> xr;
+    WRaw<ENC> wA, wB;
+    const uint32_t ksteps = columns / BK;
+    if constexpr (DMA) x_dma((const _Float16 *)x, in_stride, m_base, tokens, 0, pf_smem, wave, lane);
+    else xr.load(xrow, xvalid);
+    wA.load(wrow, 0, part);
+#pragma unroll
+    for (uint32_t c = 0; c < 4; ++c) {
+        if constexpr (!DMA) xr.store(pf_smem + srow * LDS_PITCH + part * 32, c);
+        wA.dequant(0, part, c, pf_smem + 2 * XS + srow * LDS_PITCH);
+    }
+    if (ksteps > 1) wA.load(wrow, 1, part);
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+
+    // One K step; a macro rather than a lambda so the accumulators stay in
+    // registers (a capturing lambda takes their address).
+#define NUQ_PF_STEP(KS, WNEXT, WFAR)                                                                               \
+    {                                                                                                              \
+        const uint32_t ks_ = (KS);                                                                                 \
+        const uint32_t cur = ks_ & 1;                                                                              \
+        const bool next = ks_ + 1 < ksteps;                                                                        \
+        const _Float16 *xa = pf_smem + cur * XS + (wm * 128 + (lane & 31)) * LDS_PITCH + 8 * (lane >> 5);         \
+        const _Float16 *wb = pf_smem + 2 * XS + cur * WS + (wn * 64 + (lane & 31)) * LDS_PITCH + 8 * (lane >> 5); \
+        _Float16 *wdst = pf_smem + 2 * XS + (cur ^ 1) * WS + srow * LDS_PITCH;                                     \
+        half8 fa[2][4], fb[2][2];                                                                                  \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) fa[0][i] = *(const half8 *)(xa + i * 32 * LDS_PITCH);        \
+        _Pragma("unroll") for (int j = 0; j < 2; ++j) fb[0][j] = *(const half8 *)(wb + j * 32 * LDS_PITCH);        \
+        if (ks_ + 2 < ksteps) WFAR.load(wrow, ks_ + 2, part);                                        \
+        if (next) {                                                                                  \
+            if constexpr (DMA)                                                                                     \
+                x_dma((const _Float16 *)x, in_stride, m_base, tokens, (ks_ + 1) * BK, pf_smem + (cur ^ 1) * XS,   \
+                      wave, lane);                                                                                 \
+            else                                                                                                   \
+                xr.load(xrow + (ks_ + 1) * BK, xvalid);                                                            \
+        }                                                                                                          \
+        _Pragma("unroll") for (uint32_t kk = 0; kk < BK / 16; ++kk) {                                              \
+            const uint32_t p_ = kk & 1;                                                                            \
+            if (kk + 1 < BK / 16) {                                                                                \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                      \
+                    fa[p_ ^ 1][i] = *(const half8 *)(xa + i * 32 * LDS_PITCH + (kk + 1) * 16);                     \
+                _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                      \
+                    fb[p_ ^ 1][j] = *(const half8 *)(wb + j * 32 * LDS_PITCH + (kk + 1) * 16);                     \
+            }                                                                                                      \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j) \
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[p_][i], fb[p_][j], acc[i][j], 0, 0, 0);      \
+            /* the last step dequantises into the idle buffer; harmless */                                         \
+            WNEXT.dequant(ks_ + 1, part, kk, wdst);                                                \
+        }                                                                                                          \
+        if (!DMA && next) {                                                                                        \
+            _Float16 *xdst = pf_smem + (cur ^ 1) * XS + srow * LDS_PITCH + part * 32;                              \
+            _Pragma("unroll") for (uint32_t c = 0; c < 4; ++c) xr.store(xdst, c);                                  \
+        }                                                                                                          \
+        if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70); /* vmcnt(0): this step's DMA has landed */         \
+        __syncthreads();                                                                          \
+    }
+    for (uint32_t ks = 0; ks < ksteps; ++ks) {
+        NUQ_PF_STEP(ks, wA, wB)
+        wA = wB;
+    }
+#undef NUQ_PF_STEP
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t n = n_base + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m_base + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < tokens && n < rows) y[(uint64_t)m * out_stride + n] = acc[i][j][r];
+            }
+        }
+}
+
+template <uint32_t ENC>
+static hipError_t launch_prefill(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
+                                 const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
+                                 uint32_t tokens) {
+    const uint32_t tiles = ((tokens + PF_BM - 1) / PF_BM) * ((rows + PF_BN - 1) / PF_BN);
+    const size_t lds = (size_t)2 * (PF_BM + PF_BN) * LDS_PITCH * sizeof(_Float16);
+    if (x_f16)
+        hipLaunchKernelGGL((prefill_kernel<ENC, _Float16>), dim3(tiles), dim3(PF_THREADS), lds, s, w, stride, rows,
+                           columns, (const _Float16 *)x, in_stride, y, out_stride, tokens);
+    else
+        hipLaunchKernelGGL((prefill_kernel<ENC, float>), dim3(tiles), dim3(PF_THREADS), lds, s, w, stride, rows,
+                           columns, (const float *)x, in_stride, y, out_stride, tokens);
+    return hipGetLastError();
+}
+
 template <uint32_t ENC>
 static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                   const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
@@ -199,6 +513,13 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens) {
+    if (tokens > 128) {
+        switch (encoding) {
+        case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        case 14: return launch_prefill<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        default: return launch_prefill<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        }
+    }
     switch (encoding) {
     case 12: return launch_tile_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
     case 14: return launch_tile_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);

@@ -224,6 +224,8 @@ TILE_CASES = [
     (12, 512, 5120, 8), (14, 512, 5120, 8), (8, 512, 4096, 8),
     (12, 256, 1280, 37), (14, 256, 1280, 20), (8, 256, 1280, 5),
     (12, 1024, 5120, 130), (14, 520, 17408, 64), (12, 136, 17408, 200),
+    # prefill tile (tokens > 128): ragged token and row tiles
+    (14, 520, 5120, 300), (8, 264, 4096, 257), (12, 512, 1280, 512),
 ]
 
 
