@@ -496,6 +496,187 @@ static hipError_t launch_prefill(hipStream_t s, const uint8_t *w, uint64_t strid
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Verify tile (tokens <= 16): weights dequantised straight into MFMA
+// A-fragment registers, no LDS for weights.
+//
+// v_mfma_f32_16x16x32_f16: A = 16 weight rows x 32 k (lane l: row l%16,
+// 8 consecutive k slots 8*(l/16)..+8), B = 32 k x 16 tokens (lane l: token
+// l%16, the same 8 k slots), D = 16 rows x 16 tokens. The k index is a sum
+// index, so any permutation applied to both operands leaves D unchanged:
+// lane (row r, quarter h = l/16) takes 64 values of block b that are cheap
+// for it to decode (Q4_K: qs pair h, both nibbles; Q6_K: half h/2, columns
+// 16*(h&1)..+16 of all four quarters; Q8_0: the two 32-blocks 2h, 2h+1) as
+// 8 chunks of 8 consecutive columns, and the B fragment loads the same
+// columns of x. A workgroup covers 16 rows; its waves take interleaved
+// blocks and meet in LDS.
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <uint32_t ENC>
+struct VLane;
+
+template <>
+struct VLane<12> {
+    static constexpr uint32_t BLOCK_BYTES = 144, BLOCK_VALUES = 256;
+    // first column (within the block) of chunk c for quarter h
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return 32 * (2 * h + (c >> 2)) + 8 * (c & 3); }
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&a)[8]) {
+        const uint4 hdr = *(const uint4 *)blk;
+        const uint4 q0 = *(const uint4 *)(blk + 16 + 32 * h), q1 = *(const uint4 *)(blk + 32 + 32 * h);
+        const float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * h, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+        q4k_scale_min(2 * h + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+        const float mul0 = d * (float)sc0, off0 = dmin * (float)m0;
+        const float mul1 = d * (float)sc1 * 0.0625f, off1 = dmin * (float)m1;
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // chunk c: columns 8c..8c+7 of group 2h (low nibbles), c+4: group 2h+1
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t lo = opaque_and<0x0f0f0f0fu>(w[2 * c + k]), hi = opaque_and<0xf0f0f0f0u>(w[2 * c + k]);
+                a[c][4 * k + 0] = (_Float16)fmaf(mul0, ubyte_f<0>(lo), -off0);
+                a[c][4 * k + 1] = (_Float16)fmaf(mul0, ubyte_f<1>(lo), -off0);
+                a[c][4 * k + 2] = (_Float16)fmaf(mul0, ubyte_f<2>(lo), -off0);
+                a[c][4 * k + 3] = (_Float16)fmaf(mul0, ubyte_f<3>(lo), -off0);
+                a[c + 4][4 * k + 0] = (_Float16)fmaf(mul1, ubyte_f<0>(hi), -off1);
+                a[c + 4][4 * k + 1] = (_Float16)fmaf(mul1, ubyte_f<1>(hi), -off1);
+                a[c + 4][4 * k + 2] = (_Float16)fmaf(mul1, ubyte_f<2>(hi), -off1);
+                a[c + 4][4 * k + 3] = (_Float16)fmaf(mul1, ubyte_f<3>(hi), -off1);
+            }
+        }
+    }
+};
+
+template <>
+struct VLane<14> {
+    static constexpr uint32_t BLOCK_BYTES = 210, BLOCK_VALUES = 256;
+    // chunk c: quarter q = c/2, columns 16*(h&1) + 8*(c&1) .. +8 of half h/2
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) {
+        return 128 * (h >> 1) + 32 * (c >> 1) + 16 * (h & 1) + 8 * (c & 1);
+    }
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&a)[8]) {
+        const uint32_t hf = h >> 1, l0 = 16 * (h & 1);
+        uint32_t qa[4], qb[4], qh[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            qa[k] = load_u32_unaligned(blk + hf * 64 + l0 + 4 * k);       // quarters 0 (low) / 2 (high nibble)
+            qb[k] = load_u32_unaligned(blk + hf * 64 + 32 + l0 + 4 * k);  // quarters 1 / 3
+            qh[k] = load_u32_unaligned(blk + 128 + hf * 32 + l0 + 4 * k);
+        }
+        const uint32_t s0 = load_u32_unaligned(blk + 192 + hf * 8), s1 = load_u32_unaligned(blk + 196 + hf * 8);
+        const float d = half_bits(load_u16_bytes(blk + 208));
+        const uint32_t odd = (h & 1) ? 8u : 0u;
+        float mul[4];
+        mul[0] = d * (float)(int8_t)((s0 >> odd) & 0xff);
+        mul[1] = d * (float)(int8_t)((s0 >> (16 + odd)) & 0xff);
+        mul[2] = d * (float)(int8_t)((s1 >> odd) & 0xff);
+        mul[3] = d * (float)(int8_t)((s1 >> (16 + odd)) & 0xff);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t low = (q & 1) ? qb[k] : qa[k];
+                const uint32_t u = opaque_and<0x0f0f0f0fu>(q >= 2 ? (low >> 4) : low) |
+                                   opaque_and<0x30303030u>((qh[k] >> (2 * q)) << 4);
+                const int c = 2 * q + (k >> 1), e0 = 4 * (k & 1);
+                a[c][e0 + 0] = (_Float16)fmaf(mul[q], ubyte_f<0>(u), -32.f * mul[q]);
+                a[c][e0 + 1] = (_Float16)fmaf(mul[q], ubyte_f<1>(u), -32.f * mul[q]);
+                a[c][e0 + 2] = (_Float16)fmaf(mul[q], ubyte_f<2>(u), -32.f * mul[q]);
+                a[c][e0 + 3] = (_Float16)fmaf(mul[q], ubyte_f<3>(u), -32.f * mul[q]);
+            }
+        }
+    }
+};
+
+template <>
+struct VLane<8> {
+    // a "block" here is 8 Q8_0 blocks (256 columns); quarter h = 32-blocks 2h, 2h+1
+    static constexpr uint32_t BLOCK_BYTES = 8 * 34, BLOCK_VALUES = 256;
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return 64 * h + 8 * c; }
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&a)[8]) {
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            const uint8_t *p = blk + (2 * h + bb) * 34;
+            const float d = half_bits(load_u16_bytes(p));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t v = load_u32_unaligned(p + 2 + 4 * k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[4 * bb + (k >> 1)][4 * (k & 1) + e] = (_Float16)(d * (float)(int8_t)((v >> (8 * e)) & 0xff));
+            }
+        }
+    }
+};
+
+constexpr int VF_MAX_WAVES = 16;
+
+template <uint32_t ENC, typename XT>
+__global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+                                                                    uint32_t rows, uint32_t nblocks,
+                                                                    const XT *__restrict__ x, uint64_t in_stride,
+                                                                    float *__restrict__ y, uint64_t out_stride,
+                                                                    uint32_t tokens) {
+    __shared__ float part_sums[VF_MAX_WAVES][16][16];
+    using L = VLane<ENC>;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t r16 = lane & 15, h = lane >> 4;
+    const uint32_t row0 = blockIdx.x * 16;
+    const uint8_t *wrow = w + (uint64_t)min(row0 + r16, rows - 1) * stride;
+    const bool tok_ok = r16 < tokens;
+    const XT *xrow = x + (uint64_t)(tok_ok ? r16 : 0) * in_stride;
+
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t b = wv; b < nblocks; b += nwaves) {
+        half8 a[8];
+        L::dequant(wrow + (uint64_t)b * L::BLOCK_BYTES, h, a);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            half8 bx;
+            const uint32_t col = b * L::BLOCK_VALUES + L::col(h, c);
+            if constexpr (sizeof(XT) == 2) {
+                bx = tok_ok ? *(const half8 *)((const _Float16 *)xrow + col) : half8{};
+            } else {
+                float4 f0 = tok_ok ? *(const float4 *)((const float *)xrow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 f1 = tok_ok ? *(const float4 *)((const float *)xrow + col + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                bx[0] = (_Float16)f0.x; bx[1] = (_Float16)f0.y; bx[2] = (_Float16)f0.z; bx[3] = (_Float16)f0.w;
+                bx[4] = (_Float16)f1.x; bx[5] = (_Float16)f1.y; bx[6] = (_Float16)f1.z; bx[7] = (_Float16)f1.w;
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], bx, acc, 0, 0, 0);
+        }
+    }
+    // D layout: lane l holds token l%16, rows 4*(l/16) + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part_sums[wv][4 * h + i][r16] = acc[i];
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+        const uint32_t rr = idx >> 4, t = idx & 15;
+        float v = 0.f;
+        for (uint32_t k = 0; k < nwaves; ++k) v += part_sums[k][rr][t];
+        if (t < tokens && row0 + rr < rows) y[(uint64_t)t * out_stride + row0 + rr] = v;
+    }
+}
+
+template <uint32_t ENC>
+static hipError_t launch_verify_enc(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
+                                    uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                                    uint64_t out_stride, uint32_t tokens) {
+    const uint32_t nblocks = columns / 256;
+    // waves: as few as keep the per-wave block count at its minimum
+    // ceil(nblocks / 16), so the blocks split as evenly as possible
+    const uint32_t per_wave = (nblocks + VF_MAX_WAVES - 1) / VF_MAX_WAVES;
+    const uint32_t waves = (nblocks + per_wave - 1) / per_wave;
+    dim3 grid((rows + 15) / 16), block(64 * waves);
+    if (x_f16)
+        hipLaunchKernelGGL((verify_kernel<ENC, _Float16>), grid, block, 0, s, w, stride, rows, nblocks,
+                           (const _Float16 *)x, in_stride, y, out_stride, tokens);
+    else
+        hipLaunchKernelGGL((verify_kernel<ENC, float>), grid, block, 0, s, w, stride, rows, nblocks,
+                           (const float *)x, in_stride, y, out_stride, tokens);
+    return hipGetLastError();
+}
+
 template <uint32_t ENC>
 static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                   const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
@@ -513,6 +694,13 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens) {
+    if (tokens <= 16 && columns % 256 == 0) {
+        switch (encoding) {
+        case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        case 14: return launch_verify_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        default: return launch_verify_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        }
+    }
     if (tokens > 128) {
         switch (encoding) {
         case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
