@@ -138,6 +138,33 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
             "frac_f16_peak": flops / s / 1e12 / F16_PEAK_TFLOPS}
 
 
+def bench_layer(torch, nq, backend, stream, reps=20):
+    """Configuration 3: one decode step (q/k/v, o, gate/up, down Q4_K + Q6_K
+    lm_head, M=1) captured as a HIP graph; GB/s of weight bytes per step."""
+    from nuclis_amd import layer as L
+    from nuclis_amd.synth import gaussian
+    weights = L.quantized_weights()
+    dev = L.upload(weights)
+    x = torch.from_numpy(gaussian(20, L.HIDDEN)).cuda()
+    with torch.cuda.stream(stream):
+        L.step(backend, dev, x)
+        eager = dev.buffers["logits"].clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            L.step(backend, dev, x)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dev.buffers["logits"], eager), "graph replay differs from the eager step"
+        with Timer(torch, stream) as t:
+            for _ in range(reps):
+                graph.replay()
+        token = backend.argmax(dev.buffers["logits"])
+    s = t.ms / 1e3 / reps
+    nbytes = L.weight_bytes(weights)
+    return {"us_per_step": s * 1e6, "weight_bytes": nbytes, "weight_gbs": nbytes / s / 1e9, "token": token}
+
+
 def cpu_baseline(w, x_host, rows, columns, seconds):
     from oracle import oracle as orc
     threads = orc.default_threads()
@@ -191,6 +218,7 @@ def main():
                                    if k not in ("w", "x", "y0")}
         extras["q6k_lmhead_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q6_K, 151936, 5120,
                                                                    64, 8).items() if k not in ("w", "x", "y0")}
+        extras["decode_layer_step"] = bench_layer(torch, nq, backend, stream)
         extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
                                                              args.steps, args.warmup).items()
                                if k not in ("w", "x", "y0")}
