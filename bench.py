@@ -252,7 +252,7 @@ def main():
                    "parity_normwise": normwise},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_q4k_kernel<4>",
+                     "traffic": None, "kernel": "gemv_q4k_int_kernel<2, 4>",
                      "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
         "cpu_baseline": cpu,
     }

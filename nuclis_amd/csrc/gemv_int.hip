@@ -171,9 +171,9 @@ __device__ __forceinline__ float quarter_sum(float v) {
 // computed. Per-wave row partials meet in LDS and are summed in wave order,
 // so the result does not depend on timing.
 constexpr int GI_WG_THREADS = 1024;
-constexpr uint32_t GI_MAX_SET_WAVES = 16;  // nblocks <= 64 (K <= 16384)
+constexpr uint32_t GI_MAX_SET_WAVES = 16;  // nblocks <= 128 (K <= 32768)
 
-template <int R>
+template <int R, int SLOTS>
 __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
@@ -187,13 +187,16 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t sets = (blockDim.x >> 6) / set_waves;
     const uint32_t set = wv / set_waves, kw = wv % set_waves;
-    const uint32_t g = lane >> 4, slot = (lane >> 2) & 3, j = lane & 3;
+    // lane = (row group g, block slot, pair j); a group of 4*SLOTS lanes
+    // covers SLOTS consecutive blocks
+    const uint32_t g = lane / (4 * SLOTS), slot = (lane >> 2) % SLOTS, j = lane & 3;
+    constexpr uint32_t GROUPS = 64 / (4 * SLOTS);
     const bool direct = j < 2;
     const uint32_t shift = direct ? 16 * j : 16 * j - 32;
     const uint32_t row_begin = blockIdx.x * rows_per_wg;
     const uint32_t row_end = min(row_begin + rows_per_wg, rows);
-    const uint32_t step_rows = 4 * R;
-    const uint32_t b = 4 * kw + slot;
+    const uint32_t step_rows = GROUPS * R;
+    const uint32_t b = SLOTS * kw + slot;
     const bool live = b < nblocks;
     const uint32_t boff = (live ? b : 0) * 144;
 
@@ -231,9 +234,11 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     auto compute_step = [&](uint32_t r0, const uint4 (&h)[R], const uint4 (&q0)[R], const uint4 (&q1)[R]) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float v = quarter_sum(poison + q4k_lane(h[r], q0[r], q1[r], xa, xb, shift, direct));
+            float v = poison + q4k_lane(h[r], q0[r], q1[r], xa, xb, shift, direct);
+#pragma unroll
+            for (uint32_t off = 2 * SLOTS; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
             const uint32_t row = r0 + g * R + r;
-            if ((lane & 15) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v;
+            if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v;
         }
     };
     uint32_t r0 = first;
@@ -257,17 +262,17 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
 
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
-template <int R>
+template <int R, int SLOTS>
 static hipError_t launch_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                                  const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu) {
-    const uint32_t set_waves = cdiv(nblocks, 4);
+    const uint32_t set_waves = cdiv(nblocks, SLOTS);
     uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
     if (sets_wanted && sets_wanted < sets) sets = sets_wanted;
-    const uint32_t step_rows = 4 * R;
+    const uint32_t step_rows = (64 / (4 * SLOTS)) * R;
     const uint32_t rows_per_wg = cdiv(cdiv(rows, 256 * wgs_per_cu), step_rows) * step_rows;
     const size_t lds = (size_t)nblocks * 8 * SLICE_WORDS * 4 + (size_t)rows_per_wg * set_waves * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_q4k_int_kernel<R>), dim3(cdiv(rows, rows_per_wg)), dim3(64 * set_waves * sets), lds, s,
+    hipLaunchKernelGGL((gemv_q4k_int_kernel<R, SLOTS>), dim3(cdiv(rows, rows_per_wg)), dim3(64 * set_waves * sets), lds, s,
                        w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
     return hipGetLastError();
 }
@@ -279,7 +284,7 @@ static hipError_t launch_q4k_int(hipStream_t s, const uint8_t *w, uint64_t strid
 hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                const float *x, float *y, int config) {
     const uint32_t nblocks = columns / 256;
-    if (cdiv(nblocks, 4) > GI_MAX_SET_WAVES) return hipErrorInvalidValue;
+    if (cdiv(nblocks, 8) > GI_MAX_SET_WAVES) return hipErrorInvalidValue;
     int R = config / 100, sets = (config / 10) % 10, per_cu = config % 10;
     if (config <= 0) {
         R = 2;
@@ -287,8 +292,13 @@ hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride,
         per_cu = 1;
     }
     if (per_cu == 0) per_cu = 1;
-    if (R == 1) return launch_q4k_int<1>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
-    return launch_q4k_int<2>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+    // 4 blocks per row group while a row fits in 16 waves, else 8
+    if (cdiv(nblocks, 4) <= GI_MAX_SET_WAVES) {
+        if (R == 1) return launch_q4k_int<1, 4>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+        return launch_q4k_int<2, 4>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+    }
+    if (R == 1) return launch_q4k_int<1, 8>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+    return launch_q4k_int<2, 8>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
 }
 
 }  // namespace nuq
