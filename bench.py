@@ -45,6 +45,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default="", help="comma list: gemv,prefill")
+    p.add_argument("--profile-copy", action="store_true",
+                   help="also run one plain 256 MiB device copy (the calibration kernel for rocprofv3 byte counters)")
     return p.parse_args()
 
 
@@ -165,6 +167,18 @@ def bench_layer(torch, nq, backend, stream, reps=20):
     return {"us_per_step": s * 1e6, "weight_bytes": nbytes, "weight_gbs": nbytes / s / 1e9, "token": token}
 
 
+def measured_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
+    copy-kernel calibrated) and recorded in profiles/<name>.md; None if absent."""
+    path = ROOT / "profiles" / f"{name}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(w, x_host, rows, columns, seconds):
     from oracle import oracle as orc
     threads = orc.default_threads()
@@ -197,6 +211,12 @@ def main():
     backend = nq.Backend(0)
     stream = torch.cuda.Stream()
     only = set(filter(None, args.only.split(",")))
+    if args.profile_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     rows, columns = 17408, 5120
     out = {}
     g = bench_gemv(torch, nq, backend, stream, nq.Q4_K, rows, columns, args.steps, args.warmup)
@@ -252,7 +272,7 @@ def main():
                    "parity_normwise": normwise},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_q4k_int_kernel<2, 4>",
+                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_q4k_int_kernel<2, 4>",
                      "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
         "cpu_baseline": cpu,
     }
