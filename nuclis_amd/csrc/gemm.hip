@@ -691,6 +691,19 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
     return hipGetLastError();
 }
 
+static uint32_t compute_units() {
+    static uint32_t cached = 0;
+    if (!cached) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cached = (uint32_t)n;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens) {
@@ -702,11 +715,27 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
         }
     }
     if (tokens > 128) {
-        switch (encoding) {
-        case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        case 14: return launch_prefill<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        default: return launch_prefill<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        // The 256x256 tiles of the prefill kernel come in rounds of one per
+        // CU. When the tile count leaves a partial last round, the rows that
+        // would form it go to the 128x128 tile in a second launch instead
+        // (a quarter-size round), so no round is mostly idle.
+        const uint32_t tm = (tokens + PF_BM - 1) / PF_BM, tn = (rows + PF_BN - 1) / PF_BN;
+        const uint32_t cus = compute_units();
+        uint32_t big_rows = rows;
+        if ((uint64_t)tm * tn > cus && ((uint64_t)tm * tn) % cus != 0) {
+            const uint64_t full = ((uint64_t)tm * tn) / cus * cus;  // tiles in whole rounds
+            if (full % tm == 0) big_rows = (uint32_t)(full / tm) * PF_BN;
         }
+        hipError_t e;
+        switch (encoding) {
+        case 12: e = launch_prefill<12>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
+        case 14: e = launch_prefill<14>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
+        default: e = launch_prefill<8>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
+        }
+        if (e != hipSuccess || big_rows == rows) return e;
+        w += (uint64_t)big_rows * stride;
+        y += big_rows;
+        rows -= big_rows;
     }
     switch (encoding) {
     case 12: return launch_tile_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
