@@ -28,6 +28,7 @@ struct nuq_context {
     bool generic_only = false;
     std::string last_error;
     uint32_t *argmax_buf = nullptr;  // device: {index, nonfinite flag}
+    nuq::SplitScratch split{nullptr, 0};  // prefill K-split workspace
 };
 
 namespace {
@@ -158,7 +159,7 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
                          "multi-token gemv launch");
     return hip_check(ctx,
                      nuq::launch_tile(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
-                                      (uint32_t)m->columns, x, f16, in_stride, out, out_stride, tokens),
+                                      (uint32_t)m->columns, x, f16, in_stride, out, out_stride, tokens, ctx->split),
                      "tile launch");
 }
 
@@ -199,6 +200,14 @@ nuq_context *nuq_create(int device, char *err, size_t cap) {
         delete ctx;
         return nullptr;
     }
+    // Four partial 256x256 F32 tiles per CU: 256 MiB on 256 CUs.
+    const uint32_t tiles = nuq::split_scratch_tiles();
+    if (hipMalloc((void **)&ctx->split.work, (size_t)tiles * 256 * 256 * sizeof(float)) != hipSuccess) {
+        report("hipMalloc of the prefill workspace failed");
+        nuq_destroy(ctx);
+        return nullptr;
+    }
+    ctx->split.tiles = tiles;
     return ctx;
 }
 
@@ -206,6 +215,7 @@ void nuq_destroy(nuq_context *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->argmax_buf) (void)hipFree(ctx->argmax_buf);
+    if (ctx->split.work) (void)hipFree(ctx->split.work);
     delete ctx;
 }
 

@@ -13,6 +13,8 @@
 // 32x32x16 MFMA (lane l: row l%32, k = 8*(l/32)..+8), so each operand
 // fragment is one 16-byte LDS read. Rows are padded by 8 halves to spread
 // the 32 rows of a fragment over the LDS banks.
+#include <algorithm>
+
 #include "formats.h"
 #include "kernels.h"
 
@@ -373,14 +375,31 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__re
                                                               uint32_t rows, uint32_t columns,
                                                               const XT *__restrict__ x, uint64_t in_stride,
                                                               float *__restrict__ y, uint64_t out_stride,
-                                                              uint32_t tokens) {
+                                                              uint32_t tokens, uint32_t full, uint32_t tail,
+                                                              uint32_t splits, float *__restrict__ work) {
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_smem[];
     // buffer b: activations at pf_smem + b*XS, weights at pf_smem + 2*XS + b*WS
     constexpr uint32_t XS = PF_BM * LDS_PITCH, WS = PF_BN * LDS_PITCH;
 
     const uint32_t tm = (tokens + PF_BM - 1) / PF_BM, tn = (rows + PF_BN - 1) / PF_BN;
+    // Workgroups [0, full) each own a whole tile. The `tail` tiles after
+    // them are split along K into `splits` column ranges of whole 256-column
+    // blocks, one workgroup each (workgroup full + s*tail + t takes range s
+    // of tile full + t), so a partial last round still spreads over the CUs.
+    uint32_t tile = blockIdx.x, split = 0;
+    const bool split_k = tile >= full;
+    if (split_k) {
+        tile = full + (blockIdx.x - full) % tail;
+        split = (blockIdx.x - full) / tail;
+        constexpr uint32_t BLOCK256 = ENC == 12 ? 144 : ENC == 14 ? 210 : 272;  // bytes per 256 columns
+        const uint32_t nb = columns / 256;
+        const uint32_t b0 = split * nb / splits, b1 = (split + 1) * nb / splits;
+        w += (uint64_t)b0 * BLOCK256;
+        x += (uint64_t)b0 * 256;
+        columns = (b1 - b0) * 256;
+    }
     uint32_t pid_m, pid_n;
-    tile_coords(blockIdx.x, tm, tn, &pid_m, &pid_n);
+    tile_coords(tile, tm, tn, &pid_m, &pid_n);
     const uint32_t m_base = pid_m * PF_BM, n_base = pid_n * PF_BN;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -468,6 +487,19 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__re
     }
 #undef NUQ_PF_STEP
 
+    if (split_k) {
+        // A split stores its partial tile in register order (coalesced);
+        // split_reduce_kernel adds the splits in order afterwards.
+        float *mine = work + (uint64_t)((tile - full) * splits + split) * (PF_BM * PF_BN);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mine[((i * 2 + j) * 16 + r) * PF_THREADS + tid] = acc[i][j][r];
+        return;
+    }
+
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -481,18 +513,91 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__re
         }
 }
 
+// Sums the K-split partial tiles of prefill_kernel in split order (the
+// order is fixed, so results do not depend on which split ran first) and
+// stores them. Thread e of tile t reads element e of each partial, which
+// holds accumulator r of fragment (i, j) of thread `tid` of the tile.
+__global__ void __launch_bounds__(256) split_reduce_kernel(const float *__restrict__ work, float *__restrict__ y,
+                                                           uint64_t out_stride, uint32_t rows, uint32_t tokens,
+                                                           uint32_t full, uint32_t splits) {
+    constexpr uint32_t TILE_F = PF_BM * PF_BN;
+    const uint32_t t = blockIdx.x / (TILE_F / 256);
+    const uint32_t e = (blockIdx.x % (TILE_F / 256)) * 256 + threadIdx.x;
+    const uint32_t tm = (tokens + PF_BM - 1) / PF_BM, tn = (rows + PF_BN - 1) / PF_BN;
+    uint32_t pid_m, pid_n;
+    tile_coords(full + t, tm, tn, &pid_m, &pid_n);
+    const uint32_t tid = e % PF_THREADS, k = e / PF_THREADS;  // k = (i*2 + j)*16 + r
+    const uint32_t i = k >> 5, j = (k >> 4) & 1, r = k & 15;
+    const uint32_t lane = tid & 63, wave = tid >> 6, wm = wave >> 2, wn = wave & 3;
+    const uint32_t n = pid_n * PF_BN + wn * 64 + j * 32 + (lane & 31);
+    const uint32_t m = pid_m * PF_BM + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const float *p = work + (uint64_t)t * splits * TILE_F + e;
+    float v = p[0];
+    for (uint32_t q = 1; q < splits; ++q) v += p[(uint64_t)q * TILE_F];
+    if (m < tokens && n < rows) y[(uint64_t)m * out_stride + n] = v;
+}
+
+static uint32_t compute_units() {
+    static uint32_t cached = 0;
+    if (!cached) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cached = (uint32_t)n;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
 template <uint32_t ENC>
 static hipError_t launch_prefill(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                  const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
-                                 uint32_t tokens) {
+                                 uint32_t tokens, const SplitScratch &scratch, uint32_t cus) {
     const uint32_t tiles = ((tokens + PF_BM - 1) / PF_BM) * ((rows + PF_BN - 1) / PF_BN);
+    // Tiles that fill whole rounds (one tile per CU) run whole. The rest
+    // (all of them when there are fewer tiles than CUs) may be split along
+    // K into s ranges of whole 256-column blocks, picked by a cost model in
+    // units of one tile's work on one 256-column block:
+    //   rounds(s) * (ceil(nb / s) + 1) + reduce(s),
+    // where rounds(s) = ceil(rem * s / cus), the +1 is a workgroup's fixed
+    // cost (pipeline fill, epilogue) and the reduce pass reads s partial
+    // tiles of 256 KiB per split tile (about 1/100 of a unit each, plus a
+    // launch). A split is taken only when it is predicted 15% faster (on
+    // MI355X it does not pay for Q4_K 17408 x 5120 at 512 tokens).
+    uint32_t full = tiles, tail = 0, splits = 1;
+    const uint32_t rem = tiles % cus;
+    if (rem != 0 && columns % 256 == 0 && scratch.work != nullptr) {
+        const uint32_t nb = columns / 256;
+        const double whole = (double)nb + 1.0;
+        double best = 0.85 * whole;
+        for (uint32_t sp = 2; sp <= std::min(nb, 16u); ++sp) {
+            if ((uint64_t)rem * sp > scratch.tiles) break;
+            const double rounds = (double)((rem * sp + cus - 1) / cus);
+            const double cost = rounds * ((double)((nb + sp - 1) / sp) + 1.0) + (double)rem * sp / 100.0 + 0.3;
+            if (cost < best) {
+                best = cost;
+                splits = sp;
+            }
+        }
+        if (splits > 1) {
+            full = tiles - rem;
+            tail = rem;
+        }
+    }
+    const uint32_t grid = full + tail * splits;
     const size_t lds = (size_t)2 * (PF_BM + PF_BN) * LDS_PITCH * sizeof(_Float16);
     if (x_f16)
-        hipLaunchKernelGGL((prefill_kernel<ENC, _Float16>), dim3(tiles), dim3(PF_THREADS), lds, s, w, stride, rows,
-                           columns, (const _Float16 *)x, in_stride, y, out_stride, tokens);
+        hipLaunchKernelGGL((prefill_kernel<ENC, _Float16>), dim3(grid), dim3(PF_THREADS), lds, s, w, stride, rows,
+                           columns, (const _Float16 *)x, in_stride, y, out_stride, tokens, full, tail, splits,
+                           scratch.work);
     else
-        hipLaunchKernelGGL((prefill_kernel<ENC, float>), dim3(tiles), dim3(PF_THREADS), lds, s, w, stride, rows,
-                           columns, (const float *)x, in_stride, y, out_stride, tokens);
+        hipLaunchKernelGGL((prefill_kernel<ENC, float>), dim3(grid), dim3(PF_THREADS), lds, s, w, stride, rows,
+                           columns, (const float *)x, in_stride, y, out_stride, tokens, full, tail, splits,
+                           scratch.work);
+    if (tail != 0)
+        hipLaunchKernelGGL(split_reduce_kernel, dim3(tail * (PF_BM * PF_BN / 256)), dim3(256), 0, s, scratch.work, y,
+                           out_stride, rows, tokens, full, splits);
     return hipGetLastError();
 }
 
@@ -691,22 +796,12 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
     return hipGetLastError();
 }
 
-static uint32_t compute_units() {
-    static uint32_t cached = 0;
-    if (!cached) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            cached = (uint32_t)n;
-        else
-            cached = 256;
-    }
-    return cached;
-}
+
+uint32_t split_scratch_tiles() { return 4 * compute_units(); }
 
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
-                       uint64_t out_stride, uint32_t tokens) {
+                       uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch) {
     if (tokens <= 16 && columns % 256 == 0) {
         switch (encoding) {
         case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
@@ -715,27 +810,12 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
         }
     }
     if (tokens > 128) {
-        // The 256x256 tiles of the prefill kernel come in rounds of one per
-        // CU. When the tile count leaves a partial last round, the rows that
-        // would form it go to the 128x128 tile in a second launch instead
-        // (a quarter-size round), so no round is mostly idle.
-        const uint32_t tm = (tokens + PF_BM - 1) / PF_BM, tn = (rows + PF_BN - 1) / PF_BN;
         const uint32_t cus = compute_units();
-        uint32_t big_rows = rows;
-        if ((uint64_t)tm * tn > cus && ((uint64_t)tm * tn) % cus != 0) {
-            const uint64_t full = ((uint64_t)tm * tn) / cus * cus;  // tiles in whole rounds
-            if (full % tm == 0) big_rows = (uint32_t)(full / tm) * PF_BN;
-        }
-        hipError_t e;
         switch (encoding) {
-        case 12: e = launch_prefill<12>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
-        case 14: e = launch_prefill<14>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
-        default: e = launch_prefill<8>(s, w, stride, big_rows, columns, x, x_f16, in_stride, y, out_stride, tokens); break;
+        case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
+        case 14: return launch_prefill<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
+        default: return launch_prefill<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
         }
-        if (e != hipSuccess || big_rows == rows) return e;
-        w += (uint64_t)big_rows * stride;
-        y += big_rows;
-        rows -= big_rows;
     }
     switch (encoding) {
     case 12: return launch_tile_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);

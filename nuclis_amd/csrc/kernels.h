@@ -23,6 +23,13 @@ struct SegmentsArgs {
     uint32_t mode;  // 0 plain, 1 silu(seg0) * seg1
 };
 
+// Device workspace for the K-split partial tiles of the prefill kernel:
+// room for `tiles` partial 256x256 F32 tiles.
+struct SplitScratch {
+    float *work;
+    uint32_t tiles;
+};
+
 hipError_t launch_dequant_rows(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint64_t first,
                                uint32_t count, uint32_t columns, float *out);
 hipError_t launch_gemv(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
@@ -40,6 +47,7 @@ int segment_rows_per_wave();
 hipError_t launch_argmax(hipStream_t s, const float *logits, uint64_t count, uint32_t *result);
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
-                       uint64_t out_stride, uint32_t tokens);
+                       uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);
+uint32_t split_scratch_tiles();
 
 }  // namespace nuq

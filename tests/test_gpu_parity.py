@@ -226,6 +226,8 @@ TILE_CASES = [
     (12, 1024, 5120, 130), (14, 520, 17408, 64), (12, 136, 17408, 200),
     # prefill tile (tokens > 128): ragged token and row tiles
     (14, 520, 5120, 300), (8, 264, 4096, 257), (12, 512, 1280, 512),
+    # 260 prefill tiles: 256 whole tiles, then 4 tiles split along K
+    (12, 33064, 1024, 257),
 ]
 
 
@@ -249,6 +251,25 @@ def test_tile_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
     backend.sync()
     want = orc.matmul(encoding, rows, columns, w, xref)
     check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, "tile")
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens", [(12, 5120, 17408, 512), (14, 2048, 5120, 1024)])
+def test_prefill_split_k_is_deterministic(backend, encoding, rows, columns, tokens):
+    """Tiles split along K are summed in split order by whichever split
+    finishes last: repeated launches must agree bit for bit."""
+    import torch
+    w = to_gpu(nq.quantize(encoding, gaussian(3, (rows, columns), 0.02)))
+    x = to_gpu(gaussian(4, (tokens, columns)).astype(np.float16))
+    m = nq.Matrix(encoding, rows, columns, w)
+    outs = []
+    for _ in range(3):
+        out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+        backend.matmul_kernel(nq.KERNEL_TILE, m, x, columns, out, rows, tokens)
+        backend.sync()
+        outs.append(out.cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
 
 
 @pytest.mark.parametrize("encoding", [8, 12, 14])
