@@ -272,7 +272,7 @@ def main():
                    "parity_normwise": normwise},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_q4k_int_kernel<2, 4>",
+                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_q4k_dma_kernel<4, 2>",
                      "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
         "cpu_baseline": cpu,
     }

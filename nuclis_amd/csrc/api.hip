@@ -105,7 +105,7 @@ int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
 // encodings on the row-per-wave kernels.
 int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, float *out) {
     if (m->encoding == NUQ_Q4_K) {
-        const int config = 0;  // R=2 rows per quarter-wave, one 15-wave workgroup per CU
+        const int config = 0;  // DMA kernel, two ring slots; register kernel when LDS is short
         hipError_t e = nuq::launch_gemv_q4k_int(ctx->stream, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
                                                 (uint32_t)m->columns, x, out, config);
         if (e != hipErrorInvalidValue) return hip_check(ctx, e, "q4_k gemv launch");

@@ -21,6 +21,8 @@
 // rows; wave w owns the block range [4P*w, 4P*w + 4P) of every row, so its
 // x slices are quantised once and reused for every row the workgroup
 // streams. Per-wave row partials meet in LDS and are summed in wave order.
+#include <algorithm>
+
 #include "formats.h"
 #include "kernels.h"
 
@@ -55,11 +57,20 @@ constexpr int SLICE_WORDS = 20;
 // halves agree on the slice maximum through one lane exchange. Writes the
 // slice image to lds[s * SLICE_WORDS ..]. Every lane of the wave must call
 // this (the exchanges are wave-wide).
-__device__ __forceinline__ void quantize_half_slice(const float *__restrict__ xp, uint32_t half, uint32_t *lds) {
+struct XHalf {
+    float4 f[4];
+};
+
+__device__ __forceinline__ void load_half_slice(const float *__restrict__ xp, uint32_t half, XHalf &h) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h.f[k] = *(const float4 *)(xp + 16 * half + 4 * k);
+}
+
+__device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t half, uint32_t *lds) {
     float v[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        float4 f = *(const float4 *)(xp + 16 * half + 4 * k);
+        const float4 f = xh.f[k];
         v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
     float amax = 0.f, sum = 0.f;
@@ -173,7 +184,7 @@ __device__ __forceinline__ float quarter_sum(float v) {
 constexpr int GI_WG_THREADS = 1024;
 constexpr uint32_t GI_MAX_SET_WAVES = 16;  // nblocks <= 128 (K <= 32768)
 
-template <int R, int SLOTS>
+template <int R, int SLOTS, int D>
 __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
@@ -199,25 +210,38 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     const uint32_t b = SLOTS * kw + slot;
     const bool live = b < nblocks;
     const uint32_t boff = (live ? b : 0) * 144;
-
-    uint4 hA[R], aA[R], bA[R], hB[R], aB[R], bB[R];
-    auto load_step = [&](uint32_t r0, uint4 (&h)[R], uint4 (&q0)[R], uint4 (&q1)[R]) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *blk = w + (uint64_t)min(r0 + g * R + r, rows - 1) * stride + boff;
-            h[r] = stream16(blk);
-            q0[r] = stream16(blk + 16 + 32 * j);
-            q1[r] = stream16(blk + 32 + 32 * j);
-        }
-    };
-    // The first step's weights are in flight while x is quantised.
     const uint32_t first = row_begin + set * step_rows;
     const uint32_t set_stride = sets * step_rows;
-    if (first < row_end) load_step(first, hA, aA, bA);
+    const uint32_t nsteps = first < row_end ? (row_end - first + set_stride - 1) / set_stride : 0;
+
+    // Issue order: this thread's first half-slice of x, then the weights of
+    // the first D steps (everything a wave streams, for the shapes this
+    // kernel is sized for), so the quantisation below waits only for x.
+    const uint32_t t0 = threadIdx.x;
+    XHalf xh;
+    if (t0 < 2 * nslices) load_half_slice(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
+
+    uint4 hq[D][R], aq[D][R], bq[D][R];
+#define NUQ_GI_LOAD(SLOT_, STEP_)                                                              \
+    _Pragma("unroll") for (int r = 0; r < R; ++r) {                                            \
+        const uint32_t row_ = first + (STEP_) * set_stride + g * R + r;                        \
+        const uint8_t *blk = w + (uint64_t)min(row_, row_end - 1) * stride + boff;             \
+        hq[SLOT_][r] = stream16(blk);                                                          \
+        aq[SLOT_][r] = stream16(blk + 16 + 32 * j);                                            \
+        bq[SLOT_][r] = stream16(blk + 32 + 32 * j);                                            \
+    }
+    // Loads are unconditional (rows past the range re-read the workgroup's
+    // last row, a cache hit): a load behind a branch makes the compiler's
+    // wait counts conservative and drains every outstanding load.
+#pragma unroll
+    for (int d = 0; d < D; ++d) NUQ_GI_LOAD(d, (uint32_t)d)
 
     // Cooperative quantisation of all of x: lane pair (2s, 2s+1) -> slice s.
-    for (uint32_t t = threadIdx.x; t < 2 * nslices; t += blockDim.x)
-        quantize_half_slice(x + (uint64_t)(t >> 1) * 32, t & 1, slices + (t >> 1) * SLICE_WORDS);
+    if (t0 < 2 * nslices) quantize_half_slice(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
+    for (uint32_t t = t0 + blockDim.x; t < 2 * nslices; t += blockDim.x) {
+        load_half_slice(x + (uint64_t)(t >> 1) * 32, t & 1, xh);
+        quantize_half_slice(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
+    }
     __syncthreads();
 
     XSlice xa, xb;
@@ -231,27 +255,37 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     }
     const float poison = xa.poison + xb.poison;
 
-    auto compute_step = [&](uint32_t r0, const uint4 (&h)[R], const uint4 (&q0)[R], const uint4 (&q1)[R]) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float v = poison + q4k_lane(h[r], q0[r], q1[r], xa, xb, shift, direct);
-#pragma unroll
-            for (uint32_t off = 2 * SLOTS; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            const uint32_t row = r0 + g * R + r;
-            if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v;
-        }
-    };
-    uint32_t r0 = first;
-    while (r0 < row_end) {
-        const uint32_t r1 = r0 + set_stride;
-        if (r1 < row_end) load_step(r1, hB, aB, bB);
-        compute_step(r0, hA, aA, bA);
-        if (r1 >= row_end) break;
-        const uint32_t r2 = r1 + set_stride;
-        if (r2 < row_end) load_step(r2, hA, aA, bA);
-        compute_step(r1, hB, aB, bB);
-        r0 = r2;
+    // Step i lives in register slot i % D; once computed, the slot takes
+    // step i + D. The main loop runs while every refill is a real step, so
+    // its loads need no branch; the last 2D steps are peeled.
+#define NUQ_GI_COMPUTE(SLOT_, STEP_)                                                                         \
+    {                                                                                                        \
+        const uint32_t r0_ = first + (STEP_) * set_stride;                                                   \
+        _Pragma("unroll") for (int r = 0; r < R; ++r) {                                                      \
+            float v = poison + q4k_lane(hq[SLOT_][r], aq[SLOT_][r], bq[SLOT_][r], xa, xb, shift, direct);    \
+            _Pragma("unroll") for (uint32_t off = 2 * SLOTS; off > 0; off >>= 1) v += __shfl_xor(v, off, 64); \
+            const uint32_t row = r0_ + g * R + r;                                                            \
+            if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v; \
+        }                                                                                                    \
     }
+    uint32_t i = 0;
+    for (; i + 2 * D <= nsteps; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            NUQ_GI_COMPUTE(d, i + d)
+            NUQ_GI_LOAD(d, i + d + D)
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (i + d < nsteps) NUQ_GI_COMPUTE(d, i + d)
+        if (i + d + D < nsteps) NUQ_GI_LOAD(d, i + d + D)
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (i + D + d < nsteps) NUQ_GI_COMPUTE(d, i + D + d)
+#undef NUQ_GI_COMPUTE
+#undef NUQ_GI_LOAD
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < row_end - row_begin; i += blockDim.x) {
         float t = 0.f;
@@ -260,9 +294,201 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     }
 }
 
+// DMA variant (R = 1). Instead of each lane loading its header and two
+// 16-byte code chunks straight from HBM (three scattered loads that touch
+// every cache line of the step about three times), each wave copies the
+// step's bytes -- GROUPS rows x SLOTS blocks, 144 contiguous 16-byte chunks
+// per step whatever SLOTS is -- into a private LDS ring with three
+// global_load_lds_dwordx4 (lane i of instruction n moves chunk 64n + i), and
+// the lanes then read their header and codes from LDS. Waves never read
+// another wave's ring, so only the wave's own vmcnt orders DMA and reads.
+constexpr uint32_t GD_STEP_CHUNKS = 144, GD_DMA_INSTRS = 3, GD_SLOT_BYTES = GD_DMA_INSTRS * 64 * 16;
+
+typedef __attribute__((address_space(3))) void gd_lds_void_t;
+typedef __attribute__((address_space(3))) uint8_t gd_lds_u8_t;
+
+// Reads a lane's header (16 bytes at p) and codes (32 bytes at p + qoff)
+// from its wave's ring once at most VM younger copies are outstanding, and
+// waits for the reads. Written as one asm block because the compiler cannot
+// tell ring slots apart and would otherwise wait for every copy in flight.
+template <int VM>
+__device__ __forceinline__ void ring_read(const uint8_t *p, uint32_t qoff, uint4 &h, uint4 &q0, uint4 &q1) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const gd_lds_u8_t *)p;
+    const uint32_t b = a + qoff;
+    u32x4_t vh, v0, v1;
+    asm volatile(
+        "s_waitcnt vmcnt(%3)\n\t"
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %5 offset:16\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(vh), "=&v"(v0), "=&v"(v1)
+        : "n"(VM), "v"(a), "v"(b)
+        : "memory");
+    h = make_uint4(vh.x, vh.y, vh.z, vh.w);
+    q0 = make_uint4(v0.x, v0.y, v0.z, v0.w);
+    q1 = make_uint4(v1.x, v1.y, v1.z, v1.w);
+}
+typedef __attribute__((address_space(1))) void gd_global_void_t;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of N lanes (16 or 32), left in every lane of the
+// group: four DPP adds within a 16-lane row (xor 1, xor 2, half-row mirror,
+// row mirror), then one lane exchange between rows for N = 32.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    if (N == 32) v += __shfl_xor(v, 16, 64);
+    return v;
+}
+
+template <int SLOTS, int D>
+__global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+                                                                      uint32_t rows, uint32_t nblocks,
+                                                                      uint32_t rows_per_wg, uint32_t set_waves,
+                                                                      const float *__restrict__ x,
+                                                                      float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const uint32_t nslices = nblocks * 8;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t nwaves = blockDim.x >> 6;
+    uint8_t *rings = (uint8_t *)lds;                                          // nwaves * D * GD_SLOT_BYTES
+    uint32_t *slices = lds + nwaves * D * (GD_SLOT_BYTES / 4);                // nslices * SLICE_WORDS
+    float *partial = (float *)(slices + nslices * SLICE_WORDS);               // rows_per_wg * set_waves
+    uint8_t *ring = rings + wv * D * GD_SLOT_BYTES;
+#define NUQ_GD_RING(SLOT_) (ring + (SLOT_) * GD_SLOT_BYTES)
+    const uint32_t sets = nwaves / set_waves;
+    const uint32_t set = wv / set_waves, kw = wv % set_waves;
+    const uint32_t g = lane / (4 * SLOTS), slot = (lane >> 2) % SLOTS, j = lane & 3;
+    constexpr uint32_t GROUPS = 64 / (4 * SLOTS);
+    constexpr uint32_t ROW_CHUNKS = SLOTS * 9;
+    const bool direct = j < 2;
+    const uint32_t shift = direct ? 16 * j : 16 * j - 32;
+    const uint32_t row_begin = blockIdx.x * rows_per_wg;
+    const uint32_t row_end = min(row_begin + rows_per_wg, rows);
+    const uint32_t b = SLOTS * kw + slot;
+    const bool live = b < nblocks;
+    const uint32_t first = row_begin + set * GROUPS;
+    const uint32_t set_stride = sets * GROUPS;
+    const uint32_t nsteps = first < row_end ? (row_end - first + set_stride - 1) / set_stride : 0;
+
+    // This lane's chunk in each DMA instruction: row q within the step and
+    // byte offset within the row (chunks past the step repeat the last one;
+    // blocks past the row read block 0, so every byte copied is real data).
+    uint32_t dq[GD_DMA_INSTRS], doff[GD_DMA_INSTRS];
+#pragma unroll
+    for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {
+        const uint32_t k = min(64 * n + lane, GD_STEP_CHUNKS - 1);
+        const uint32_t c = k % ROW_CHUNKS, blk = SLOTS * kw + c / 9;
+        dq[n] = k / ROW_CHUNKS;
+        doff[n] = (blk < nblocks ? blk * 144 : 0) + 16 * (c % 9);
+    }
+#define NUQ_GD_DMA(SLOT_, STEP_)                                                                              \
+    _Pragma("unroll") for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {                                          \
+        const uint32_t row_ = min(first + (STEP_) * set_stride + dq[n], row_end - 1);                         \
+        __builtin_amdgcn_global_load_lds((gd_global_void_t *)(w + (uint64_t)row_ * stride + doff[n]),         \
+                                         (gd_lds_void_t *)(NUQ_GD_RING(SLOT_) + n * 1024), 16, 0,             \
+                                         2);                                                                  \
+    }
+
+    const uint32_t t0 = threadIdx.x;
+    XHalf xh;
+    if (t0 < 2 * nslices) load_half_slice(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
+#pragma unroll
+    for (int d = 0; d < D; ++d) NUQ_GD_DMA(d, (uint32_t)d)
+
+    if (t0 < 2 * nslices) quantize_half_slice(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
+    for (uint32_t t = t0 + blockDim.x; t < 2 * nslices; t += blockDim.x) {
+        load_half_slice(x + (uint64_t)(t >> 1) * 32, t & 1, xh);
+        quantize_half_slice(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
+    }
+    __syncthreads();
+
+    XSlice xa, xb;
+    const uint32_t bb = live ? b : 0;
+    read_slice(slices + (bb * 8 + 2 * j) * SLICE_WORDS, xa);
+    read_slice(slices + (bb * 8 + 2 * j + 1) * SLICE_WORDS, xb);
+    if (!live) {
+        xa.scale = xb.scale = 0.f;
+        xa.sum = xb.sum = 0.f;
+        xa.poison = xb.poison = 0.f;
+    }
+    const float poison = xa.poison + xb.poison;
+    const uint32_t role = (g * ROW_CHUNKS + slot * 9) * 16;
+
+    // Step i lives in ring slot i % D. As soon as a slot's bytes are in
+    // registers the slot is refilled with step i + D, before the arithmetic.
+    // In the main loop the D-1 younger steps' copies (3 each) may still be in
+    // flight when slot d is read; the peeled tail issues fewer copies, so it
+    // waits for all of them.
+#define NUQ_GD_COMPUTE(SLOT_, STEP_, VM_, REFILL_)                                                                     \
+    {                                                                                                       \
+        uint4 h, q0, q1;                                                                                    \
+        ring_read<VM_>(NUQ_GD_RING(SLOT_) + role, 16 + 32 * j, h, q0, q1);                                  \
+        REFILL_                                                                                             \
+        const float v = group_sum<4 * SLOTS>(poison + q4k_lane(h, q0, q1, xa, xb, shift, direct));          \
+        const uint32_t row = first + (STEP_) * set_stride + g;                                              \
+        if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v; \
+    }
+    uint32_t i = 0;
+    for (; i + 2 * D <= nsteps; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            NUQ_GD_COMPUTE(d, i + d, GD_DMA_INSTRS * (D - 1), NUQ_GD_DMA(d, i + d + D))
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (i + d < nsteps) NUQ_GD_COMPUTE(d, i + d, 0, if (i + d + D < nsteps) { NUQ_GD_DMA(d, i + d + D) })
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (i + D + d < nsteps) NUQ_GD_COMPUTE(d, i + D + d, 0, )
+#undef NUQ_GD_COMPUTE
+#undef NUQ_GD_DMA
+#undef NUQ_GD_RING
+    // Copies issued for steps past the range (when nsteps < D) must land
+    // before the workgroup ends.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < row_end - row_begin; r += blockDim.x) {
+        float t = 0.f;
+        for (uint32_t k = 0; k < set_waves; ++k) t += partial[r * set_waves + k];
+        y[row_begin + r] = t;
+    }
+}
+
+template <int SLOTS, int D>
+static hipError_t launch_q4k_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
+                                 const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu) {
+    const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
+    const uint32_t step_rows = 64 / (4 * SLOTS);
+    uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
+    // Fewer wave sets for small matrices, so the grid still covers the CUs.
+    if (!sets_wanted) sets_wanted = std::max(1u, rows / (256 * wgs_per_cu * step_rows));
+    if (sets_wanted < sets) sets = sets_wanted;
+    const uint32_t unit = step_rows * sets;
+    const uint32_t per_wg = (rows + 256 * wgs_per_cu - 1) / (256 * wgs_per_cu);
+    const uint32_t rows_per_wg = (per_wg + unit - 1) / unit * unit;
+    const uint32_t waves = set_waves * sets;
+    const size_t lds = (size_t)waves * D * GD_SLOT_BYTES + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
+                       (size_t)rows_per_wg * set_waves * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_q4k_dma_kernel<SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(64 * waves),
+                       lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
+    return hipGetLastError();
+}
+
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
-template <int R, int SLOTS>
+template <int R, int SLOTS, int D>
 static hipError_t launch_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                                  const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu) {
     const uint32_t set_waves = cdiv(nblocks, SLOTS);
@@ -272,33 +498,54 @@ static hipError_t launch_q4k_int(hipStream_t s, const uint8_t *w, uint64_t strid
     const uint32_t rows_per_wg = cdiv(cdiv(rows, 256 * wgs_per_cu), step_rows) * step_rows;
     const size_t lds = (size_t)nblocks * 8 * SLICE_WORDS * 4 + (size_t)rows_per_wg * set_waves * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_q4k_int_kernel<R, SLOTS>), dim3(cdiv(rows, rows_per_wg)), dim3(64 * set_waves * sets), lds, s,
+    hipLaunchKernelGGL((gemv_q4k_int_kernel<R, SLOTS, D>), dim3(cdiv(rows, rows_per_wg)), dim3(64 * set_waves * sets), lds, s,
                        w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
     return hipGetLastError();
 }
 
-// config = R*100 + sets*10 + workgroups per CU (0 = defaults: R=2, as many
-// wave sets as fit in 16 waves, one workgroup per CU). Returns
-// hipErrorInvalidValue when the shape does not fit (more than 64 blocks per
-// row): the caller then uses the row-per-wave kernel.
+// config 0: the DMA kernel with two ring slots, or the register kernel (two
+// slots, one row per lane group) when x and the rings do not fit in LDS.
+// config >= 10000 forces the DMA kernel: 10000 + D*1000 + sets*10 + WGs/CU;
+// other values force the register kernel: D*1000 + R*100 + sets*10 + WGs/CU.
+// Returns hipErrorInvalidValue when the shape does not fit (more than 128
+// blocks per row): the caller then uses the row-per-wave kernel.
 hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                const float *x, float *y, int config) {
     const uint32_t nblocks = columns / 256;
     if (cdiv(nblocks, 8) > GI_MAX_SET_WAVES) return hipErrorInvalidValue;
-    int R = config / 100, sets = (config / 10) % 10, per_cu = config % 10;
+    if (config >= 10000 || config <= 0) {
+        // DMA kernel: config = 10000 + D*1000 + sets*10 + workgroups per CU
+        const int c = config <= 0 ? 12000 : config;
+        const int dd = (c / 1000) % 10, st = (c / 10) % 10, pc = c % 10 ? c % 10 : 1;
+        hipError_t e = hipErrorInvalidValue;
+        if (cdiv(nblocks, 4) <= GI_MAX_SET_WAVES) {
+            if (dd == 2) e = launch_q4k_dma<4, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
+            else if (dd == 3) e = launch_q4k_dma<4, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
+        } else {
+            if (dd == 2) e = launch_q4k_dma<8, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
+            else if (dd == 3) e = launch_q4k_dma<8, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
+        }
+        if (e != hipErrorInvalidValue || config > 0) return e;
+        config = 0;  // the LDS does not fit: register kernel
+    }
+    int D = config / 1000, R = (config / 100) % 10, sets = (config / 10) % 10, per_cu = config % 10;
     if (config <= 0) {
-        R = 2;
+        D = 2;
+        R = 1;
         sets = 0;
         per_cu = 1;
     }
     if (per_cu == 0) per_cu = 1;
+#define NUQ_GI_CASE(D_, R_, S_) \
+    if (D == D_ && R == R_) return launch_q4k_int<R_, S_, D_>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
     // 4 blocks per row group while a row fits in 16 waves, else 8
     if (cdiv(nblocks, 4) <= GI_MAX_SET_WAVES) {
-        if (R == 1) return launch_q4k_int<1, 4>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
-        return launch_q4k_int<2, 4>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+        NUQ_GI_CASE(2, 2, 4) NUQ_GI_CASE(2, 1, 4)
+    } else {
+        NUQ_GI_CASE(2, 2, 8) NUQ_GI_CASE(2, 1, 8)
     }
-    if (R == 1) return launch_q4k_int<1, 8>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
-    return launch_q4k_int<2, 8>(s, w, stride, rows, nblocks, x, y, sets, per_cu);
+#undef NUQ_GI_CASE
+    return hipErrorInvalidValue;
 }
 
 }  // namespace nuq

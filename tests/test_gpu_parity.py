@@ -117,6 +117,9 @@ GEMV_SHAPES = [
     (14, 35, 1280),
     (8, 35, 1280),
     (12, 1, 256),
+    (12, 257, 1024),      # one wave set, ragged last workgroup
+    (12, 100, 24576),     # 8-block lane groups on the DMA kernel
+    (12, 64, 32768),      # x and the rings exceed LDS: register kernel
 ]
 
 
