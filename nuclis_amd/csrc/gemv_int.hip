@@ -57,20 +57,54 @@ constexpr int SLICE_WORDS = 20;
 // halves agree on the slice maximum through one lane exchange. Writes the
 // slice image to lds[s * SLICE_WORDS ..]. Every lane of the wave must call
 // this (the exchanges are wave-wide).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 struct XHalf {
-    float4 f[4];
+    f32x4_t f[4];
 };
 
 __device__ __forceinline__ void load_half_slice(const float *__restrict__ xp, uint32_t half, XHalf &h) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) h.f[k] = *(const float4 *)(xp + 16 * half + 4 * k);
+    for (int k = 0; k < 4; ++k) h.f[k] = *(const f32x4_t *)(xp + 16 * half + 4 * k);
 }
 
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+
+// LDS accesses written as asm, for kernels that also copy into LDS with
+// global_load_lds: the compiler cannot tell the copies' destination apart
+// from other LDS data and would wait for every copy in flight before a
+// plain LDS access. The caller orders these with explicit lgkmcnt waits.
+__device__ __forceinline__ uint32_t lds_addr(const uint32_t *p) { return (uint32_t)(uintptr_t)(const lds_u32_t *)p; }
+__device__ __forceinline__ void lds_store4(uint32_t *p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    u32x4_t v = {a, b, c, d};
+    asm volatile("ds_write_b128 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
+
+// x loads as asm, for the same reason: with copies into LDS in flight the
+// compiler waits for all of them before using any load it issued. The
+// caller waits with xhalf_wait<N>, N = loads issued after these.
+__device__ __forceinline__ void load_half_slice_asm(const float *__restrict__ xp, uint32_t half, XHalf &h) {
+    const float *p = xp + 16 * half;
+    asm volatile(
+        "global_load_dwordx4 %0, %4, off\n\t"
+        "global_load_dwordx4 %1, %4, off offset:16\n\t"
+        "global_load_dwordx4 %2, %4, off offset:32\n\t"
+        "global_load_dwordx4 %3, %4, off offset:48"
+        : "=&v"(h.f[0]), "=&v"(h.f[1]), "=&v"(h.f[2]), "=&v"(h.f[3])
+        : "v"(p)
+        : "memory");
+}
+template <int N>
+__device__ __forceinline__ void xhalf_wait(XHalf &h) {
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(h.f[0]), "+v"(h.f[1]), "+v"(h.f[2]), "+v"(h.f[3]) : "n"(N) : "memory");
+}
+
+template <bool ASM_LDS = false>
 __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t half, uint32_t *lds) {
     float v[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const float4 f = xh.f[k];
+        const f32x4_t f = xh.f[k];
         v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
     float amax = 0.f, sum = 0.f;
@@ -88,6 +122,7 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
     const float scale = amax / 32639.f;
     const float inv = amax > 0.f ? 32639.f / amax : 0.f;
     int isum = 0;
+    uint32_t hw[4], lw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         uint32_t h = 0, l = 0;
@@ -100,16 +135,54 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
             h |= (uint32_t)(hi & 255) << (8 * e);
             l |= (uint32_t)(lo & 255) << (8 * e);
         }
-        lds[4 * half + k] = h;
-        lds[8 + 4 * half + k] = l;
+        hw[k] = h;
+        lw[k] = l;
     }
     isum += __shfl_xor(isum, 1, 64);
-    if (half == 0) {
-        lds[16] = __float_as_uint(scale);
-        lds[17] = __float_as_uint(sum + other_sum);  // lower half first, as the summation order
-        lds[18] = (uint32_t)isum;
-        lds[19] = finite ? 0u : 0x7fc00000u;
+    // words: hi plane 0..7, lo plane 8..15, then scale, sum (lower half first, as
+    // the summation order), isum, poison
+    const uint32_t t0 = __float_as_uint(scale), t1 = __float_as_uint(sum + other_sum), t2 = (uint32_t)isum,
+                   t3 = finite ? 0u : 0x7fc00000u;
+    if constexpr (ASM_LDS) {
+        lds_store4(lds + 4 * half, hw[0], hw[1], hw[2], hw[3]);
+        lds_store4(lds + 8 + 4 * half, lw[0], lw[1], lw[2], lw[3]);
+        if (half == 0) lds_store4(lds + 16, t0, t1, t2, t3);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lds[4 * half + k] = hw[k];
+            lds[8 + 4 * half + k] = lw[k];
+        }
+        if (half == 0) {
+            lds[16] = t0;
+            lds[17] = t1;
+            lds[18] = t2;
+            lds[19] = t3;
+        }
     }
+}
+
+// read_slice through asm (see lds_store4); waits for its own reads.
+__device__ __forceinline__ void read_slice_asm(const uint32_t *lds, XSlice &s) {
+    u32x4_t a, b, c, d, e;
+    asm volatile(
+        "ds_read_b128 %0, %5\n\t"
+        "ds_read_b128 %1, %5 offset:16\n\t"
+        "ds_read_b128 %2, %5 offset:32\n\t"
+        "ds_read_b128 %3, %5 offset:48\n\t"
+        "ds_read_b128 %4, %5 offset:64\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d), "=&v"(e)
+        : "v"(lds_addr(lds))
+        : "memory");
+    s.hi[0] = a.x; s.hi[1] = a.y; s.hi[2] = a.z; s.hi[3] = a.w;
+    s.hi[4] = b.x; s.hi[5] = b.y; s.hi[6] = b.z; s.hi[7] = b.w;
+    s.lo[0] = c.x; s.lo[1] = c.y; s.lo[2] = c.z; s.lo[3] = c.w;
+    s.lo[4] = d.x; s.lo[5] = d.y; s.lo[6] = d.z; s.lo[7] = d.w;
+    s.scale = __uint_as_float(e.x);
+    s.sum = __uint_as_float(e.y);
+    s.isum = (int)e.z;
+    s.poison = __uint_as_float(e.w);
 }
 
 __device__ __forceinline__ void read_slice(const uint32_t *lds, XSlice &s) {
@@ -400,21 +473,26 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
 
     const uint32_t t0 = threadIdx.x;
     XHalf xh;
-    if (t0 < 2 * nslices) load_half_slice(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
+    if (t0 < 2 * nslices) load_half_slice_asm(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
 #pragma unroll
     for (int d = 0; d < D; ++d) NUQ_GD_DMA(d, (uint32_t)d)
 
-    if (t0 < 2 * nslices) quantize_half_slice(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
+    // The slice image goes to LDS through asm and the barrier carries no
+    // fence, so the copies in flight keep flying while x is quantised.
+    xhalf_wait<GD_DMA_INSTRS * D>(xh);  // x is older than the D steps' copies
+    if (t0 < 2 * nslices) quantize_half_slice<true>(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
     for (uint32_t t = t0 + blockDim.x; t < 2 * nslices; t += blockDim.x) {
-        load_half_slice(x + (uint64_t)(t >> 1) * 32, t & 1, xh);
-        quantize_half_slice(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
+        load_half_slice_asm(x + (uint64_t)(t >> 1) * 32, t & 1, xh);
+        xhalf_wait<0>(xh);
+        quantize_half_slice<true>(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
     }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    __builtin_amdgcn_s_barrier();
 
     XSlice xa, xb;
     const uint32_t bb = live ? b : 0;
-    read_slice(slices + (bb * 8 + 2 * j) * SLICE_WORDS, xa);
-    read_slice(slices + (bb * 8 + 2 * j + 1) * SLICE_WORDS, xb);
+    read_slice_asm(slices + (bb * 8 + 2 * j) * SLICE_WORDS, xa);
+    read_slice_asm(slices + (bb * 8 + 2 * j + 1) * SLICE_WORDS, xb);
     if (!live) {
         xa.scale = xb.scale = 0.f;
         xa.sum = xb.sum = 0.f;
