@@ -197,18 +197,22 @@ __device__ __forceinline__ void read_slice(const uint32_t *lds, XSlice &s) {
     s.poison = __uint_as_float(lds[19]);
 }
 
-// Q4_K scales/minima of the pair (2j, 2j+1) as floats (quant/decode.zig:155-158).
+// Q4_K scales/minima of the pair (2j, 2j+1) as floats (quant/decode.zig:155-158),
+// without branches: with shift = 16*(j&1), the pair's two scale bytes are
+// bytes 0-1 of A = s0>>shift (and the minima of M = s1>>shift). Pairs 0 and 1
+// use their 6 low bits; pairs 2 and 3 take the low (scales) or high (minima)
+// nibble of Z = s2>>shift plus bits 6-7 of A (or M) as bits 4-5. Both forms
+// are computed on the two bytes at once and selected with a lane mask.
 __device__ __forceinline__ void q4k_pair_f(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t shift, bool direct,
                                            float &sa, float &ma, float &sb, float &mb) {
-    const uint32_t x = s0 >> shift, y = s1 >> shift, z = s2 >> shift;
-    const uint32_t a = direct ? (x & 63u) : ((z & 15u) | (((x >> 6) & 3u) << 4));
-    const uint32_t m = direct ? (y & 63u) : (((z >> 4) & 15u) | (((y >> 6) & 3u) << 4));
-    const uint32_t b = direct ? ((x >> 8) & 63u) : (((z >> 8) & 15u) | (((x >> 14) & 3u) << 4));
-    const uint32_t n = direct ? ((y >> 8) & 63u) : (((z >> 12) & 15u) | (((y >> 14) & 3u) << 4));
-    sa = (float)a;
-    ma = (float)m;
-    sb = (float)b;
-    mb = (float)n;
+    const uint32_t A = s0 >> shift, M = s1 >> shift, Z = s2 >> shift;
+    const uint32_t dm = 0u - (uint32_t)direct;
+    const uint32_t sc = ((A & 0x3f3fu) & dm) | (((Z & 0x0f0fu) | ((A >> 2) & 0x3030u)) & ~dm);
+    const uint32_t mn = ((M & 0x3f3fu) & dm) | ((((Z >> 4) & 0x0f0fu) | ((M >> 2) & 0x3030u)) & ~dm);
+    sa = ubyte_f<0>(sc);
+    sb = ubyte_f<1>(sc);
+    ma = ubyte_f<0>(mn);
+    mb = ubyte_f<1>(mn);
 }
 
 // One lane's 64 values of one Q4_K block (qs pair j: 32 bytes) against its
@@ -434,7 +438,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     const uint32_t nwaves = blockDim.x >> 6;
     uint8_t *rings = (uint8_t *)lds;                                          // nwaves * D * GD_SLOT_BYTES
     uint32_t *slices = lds + nwaves * D * (GD_SLOT_BYTES / 4);                // nslices * SLICE_WORDS
-    float *partial = (float *)(slices + nslices * SLICE_WORDS);               // rows_per_wg * set_waves
+    float *partial = (float *)(slices + nslices * SLICE_WORDS);               // rows_per_wg * set_waves + nwaves
     uint8_t *ring = rings + wv * D * GD_SLOT_BYTES;
 #define NUQ_GD_RING(SLOT_) (ring + (SLOT_) * GD_SLOT_BYTES)
     const uint32_t sets = nwaves / set_waves;
@@ -465,11 +469,16 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     }
 #define NUQ_GD_DMA(SLOT_, STEP_)                                                                              \
     _Pragma("unroll") for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {                                          \
-        const uint32_t row_ = min(first + (STEP_) * set_stride + dq[n], row_end - 1);                         \
-        __builtin_amdgcn_global_load_lds((gd_global_void_t *)(w + (uint64_t)row_ * stride + doff[n]),         \
-                                         (gd_lds_void_t *)(NUQ_GD_RING(SLOT_) + n * 1024), 16, 0,             \
-                                         2);                                                                  \
+        const uint32_t lrow_ = min(first_local + (STEP_) * set_stride + dq[n], last_local);                   \
+        __builtin_amdgcn_global_load_lds((gd_global_void_t *)(wg_base + (lrow_ * stride32 + doff[n])),        \
+                                         (gd_lds_void_t *)(NUQ_GD_RING(SLOT_) + n * 1024), 16, 0, 2);         \
     }
+
+    // Copy addresses: a uniform workgroup base plus a 32-bit offset (the
+    // host keeps a workgroup's rows within 4 GiB).
+    const uint8_t *wg_base = w + (uint64_t)row_begin * stride;
+    const uint32_t stride32 = (uint32_t)stride;
+    const uint32_t first_local = first - row_begin, last_local = row_end - 1 - row_begin;
 
     const uint32_t t0 = threadIdx.x;
     XHalf xh;
@@ -500,6 +509,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     }
     const float poison = xa.poison + xb.poison;
     const uint32_t role = (g * ROW_CHUNKS + slot * 9) * 16;
+    const uint32_t spare = rows_per_wg * set_waves + wv;  // one spare partial per wave
 
     // Step i lives in ring slot i % D. As soon as a slot's bytes are in
     // registers the slot is refilled with step i + D, before the arithmetic.
@@ -513,7 +523,8 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
         REFILL_                                                                                             \
         const float v = group_sum<4 * SLOTS>(poison + q4k_lane(h, q0, q1, xa, xb, shift, direct));          \
         const uint32_t row = first + (STEP_) * set_stride + g;                                              \
-        if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v; \
+        /* every lane of the group holds the sum; rows past the range go to a spare slot */               \
+        partial[row < row_end ? (row - row_begin) * set_waves + kw : spare] = v;                            \
     }
     uint32_t i = 0;
     for (; i + 2 * D <= nsteps; i += D) {
@@ -557,8 +568,9 @@ static hipError_t launch_q4k_dma(hipStream_t s, const uint8_t *w, uint64_t strid
     const uint32_t rows_per_wg = (per_wg + unit - 1) / unit * unit;
     const uint32_t waves = set_waves * sets;
     const size_t lds = (size_t)waves * D * GD_SLOT_BYTES + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
-                       (size_t)rows_per_wg * set_waves * 4;
+                       ((size_t)rows_per_wg * set_waves + waves) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
     hipLaunchKernelGGL((gemv_q4k_dma_kernel<SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(64 * waves),
                        lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
     return hipGetLastError();
