@@ -344,19 +344,38 @@ typedef __attribute__((address_space(1))) void global_void_t;
 // tile (9 slots a row: 8 of data, 1 of padding, so rows keep the 144-byte
 // pitch the fragment reads want). Padding slots load a valid address and
 // are never read. Rows past `tokens` re-read the last token: their outputs
-// are never stored.
-__device__ __forceinline__ void x_dma(const _Float16 *__restrict__ x, uint64_t in_stride, uint32_t m_base,
-                                      uint32_t tokens, uint32_t k0, _Float16 *lds_tile, uint32_t wave,
-                                      uint32_t lane) {
-    constexpr uint32_t SLOTS = PF_BM * 9, INSTRS = SLOTS / 64;  // 36
-    for (uint32_t q = wave; q < INSTRS; q += PF_THREADS / 64) {
-        const uint32_t slot = 64 * q + lane;
-        const uint32_t row = slot / 9, chunk = slot % 9;
-        const uint32_t tok = min(m_base + row, tokens - 1);
-        const _Float16 *src = x + (uint64_t)tok * in_stride + k0 + 8 * (chunk == 8 ? 0 : chunk);
-        __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(lds_tile + 64 * q * 8), 16, 0, 0);
+// are never stored. Wave w issues instructions q = w, w + 8, ...: at most
+// XD_PER_WAVE. A lane's byte offsets from the tile's first row are fixed
+// for the whole K loop, so they are computed once (XDma::init) and each
+// slab's copies are a uniform base plus those offsets.
+constexpr uint32_t XD_INSTRS = PF_BM * 9 / 64, XD_PER_WAVE = (XD_INSTRS + PF_THREADS / 64 - 1) / (PF_THREADS / 64);
+struct XDma {
+    uint32_t off[XD_PER_WAVE];
+    uint32_t first;  // this wave's first instruction (scalar)
+    __device__ __forceinline__ void init(uint64_t in_stride, uint32_t m_base, uint32_t tokens, uint32_t wave,
+                                         uint32_t lane) {
+        first = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t last_row = tokens - 1 - m_base;
+#pragma unroll
+        for (uint32_t t = 0; t < XD_PER_WAVE; ++t) {
+            const uint32_t slot = 64 * (first + t * (PF_THREADS / 64)) + lane;
+            const uint32_t row = min(slot / 9, last_row), chunk = slot % 9;
+            off[t] = (uint32_t)(((uint64_t)row * in_stride + 8 * (chunk == 8 ? 0 : chunk)) * 2);
+        }
     }
-}
+    // copies columns k0..k0+63 of the tile's rows into lds_tile
+    __device__ __forceinline__ void copy(const _Float16 *__restrict__ x, uint64_t in_stride, uint32_t m_base,
+                                         uint32_t k0, _Float16 *lds_tile) const {
+        const char *base = (const char *)(x + (uint64_t)m_base * in_stride + k0);
+#pragma unroll
+        for (uint32_t t = 0; t < XD_PER_WAVE; ++t) {
+            const uint32_t q = first + t * (PF_THREADS / 64);
+            if (XD_INSTRS % (PF_THREADS / 64) != 0 && q >= XD_INSTRS) break;
+            __builtin_amdgcn_global_load_lds((global_void_t *)(base + off[t]), (lds_void_t *)(lds_tile + 64 * q * 8),
+                                             16, 0, 0);
+        }
+    }
+};
 
 __device__ __forceinline__ void tile_coords(uint32_t id, uint32_t tm, uint32_t tn, uint32_t *pid_m, uint32_t *pid_n) {
     const uint32_t total = tm * tn;
@@ -428,7 +447,11 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__re
     XLoad<XT> xr;
     WRaw<ENC> wA, wB;
     const uint32_t ksteps = columns / BK;
-    if constexpr (DMA) x_dma((const _Float16 *)x, in_stride, m_base, tokens, 0, pf_smem, wave, lane);
+    XDma xd;
+    if constexpr (DMA) {
+        xd.init(in_stride, m_base, tokens, wave, lane);
+        xd.copy((const _Float16 *)x, in_stride, m_base, 0, pf_smem);
+    }
     else xr.load(xrow, xvalid);
     wA.load(wrow, 0, part);
 #pragma unroll
@@ -456,8 +479,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_kernel(const uint8_t *__re
         if (ks_ + 2 < ksteps) WFAR.load(wrow, ks_ + 2, part);                                        \
         if (next) {                                                                                  \
             if constexpr (DMA)                                                                                     \
-                x_dma((const _Float16 *)x, in_stride, m_base, tokens, (ks_ + 1) * BK, pf_smem + (cur ^ 1) * XS,   \
-                      wave, lane);                                                                                 \
+                xd.copy((const _Float16 *)x, in_stride, m_base, (ks_ + 1) * BK, pf_smem + (cur ^ 1) * XS);        \
             else                                                                                                   \
                 xr.load(xrow + (ks_ + 1) * BK, xvalid);                                                            \
         }                                                                                                          \
@@ -809,7 +831,8 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
         default: return launch_verify_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
         }
     }
-    if (tokens > 128) {
+    // (the prefill tile's activation copies use 32-bit offsets within a tile)
+    if (tokens > 128 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {
         const uint32_t cus = compute_units();
         switch (encoding) {
         case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
