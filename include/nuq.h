@@ -7,7 +7,8 @@
  * @cImport instead of the nu_metal_* bridge (backends/metal/root.zig:29-44,
  * bridge.m). Weights are raw GGUF rows, read as-is from device memory and
  * never repacked: Q8_0 (encoding 8, 34-byte blocks of 32), Q4_K (12, 144-byte
- * blocks of 256) and Q6_K (14, 210-byte blocks of 256).
+ * blocks of 256), Q5_K (13, 176-byte blocks of 256), Q6_K (14, 210-byte blocks
+ * of 256) and IQ4_XS (23, 136-byte blocks of 256).
  *
  * Conventions (mirroring the reference):
  *  - Every function returns 0 on success or a NUQ_* status. Validation happens
@@ -44,7 +45,7 @@ enum nuq_status {
 };
 
 /* GGML encoding ids (inference/src/tensor/encoding.zig:29-41). */
-enum nuq_encoding { NUQ_Q8_0 = 8, NUQ_Q4_K = 12, NUQ_Q6_K = 14 };
+enum nuq_encoding { NUQ_Q8_0 = 8, NUQ_Q4_K = 12, NUQ_Q5_K = 13, NUQ_Q6_K = 14, NUQ_IQ4_XS = 23 };
 
 /* Activation element type of nuq_matmul. The reference passes F32
  * (ops/matmul.zig:79); F16 activations are accepted as they are. */
@@ -139,8 +140,9 @@ int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *
 /* Weight preparation on the host (not part of the reference's backend):
  * quantize `rows` F32 rows of `columns` into GGUF rows in dst (host memory,
  * dst_len = rows * row bytes). Q8_0 is quant/encode.zig:17-36 exactly; the
- * reference has no Q4_K / Q6_K quantizer (encode.zig:1-2), so those two are
- * this library's own deterministic quantizers producing legal blocks. */
+ * reference has no K-quant or IQ4_XS quantizer (encode.zig:1-2), so Q4_K,
+ * Q5_K, Q6_K and IQ4_XS use this library's own deterministic quantizers
+ * producing legal blocks. */
 int nuq_quantize_rows(uint32_t encoding, const float *src, uint64_t rows, uint64_t columns, void *dst,
                       uint64_t dst_len);
 

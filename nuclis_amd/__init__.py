@@ -4,7 +4,7 @@ The product is libnuq.so (HIP kernels + C ABI, include/nuq.h); `backend`
 mirrors the reference's Zig Backend entry points over it.
 """
 from .backend import (  # noqa: F401
-    F16, F32, KERNEL_AUTO, KERNEL_GENERIC, KERNEL_ROWS, KERNEL_TILE, LAYOUT, Q4_K, Q6_K, Q8_0, SEGMENT_PLAIN,
+    F16, F32, KERNEL_AUTO, KERNEL_GENERIC, KERNEL_ROWS, KERNEL_TILE, LAYOUT, IQ4_XS, Q4_K, Q5_K, Q6_K, Q8_0, SEGMENT_PLAIN,
     SEGMENT_SILU_MUL_PAIR, Backend, DeviceError, InvalidArgument, InvalidByteLength, InvalidRowLength, InvalidShape,
     Matrix, NonFiniteResult, NuqError, UnsupportedTensorEncoding, lib, quantize, row_bytes, validate_row,
 )

@@ -23,13 +23,13 @@ import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "libnuq.so"
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 12, 13, 14, 23
 F32, F16 = 0, 1
 KERNEL_AUTO, KERNEL_ROWS, KERNEL_TILE, KERNEL_GENERIC = 0, 1, 2, 3
 SEGMENT_PLAIN, SEGMENT_SILU_MUL_PAIR = 0, 1
 
 # inference/src/tensor/encoding.zig:29-41: id -> (values per block, bytes per block)
-LAYOUT = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+LAYOUT = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136)}
 
 
 class NuqError(Exception):
@@ -139,8 +139,8 @@ def row_bytes(encoding: int, columns: int) -> int:
 def quantize(encoding: int, weights: np.ndarray) -> np.ndarray:
     """F32 [rows][columns] -> GGUF rows (uint8 [rows][row_bytes]) on the host.
 
-    Q8_0 is the reference's q8_0Row (quant/encode.zig:17-36); Q4_K and Q6_K
-    use this library's own quantizers (the reference has none)."""
+    Q8_0 is the reference's q8_0Row (quant/encode.zig:17-36); Q4_K, Q5_K, Q6_K
+    and IQ4_XS use this library's own quantizers (the reference has none)."""
     w = np.ascontiguousarray(weights, dtype=np.float32)
     if w.ndim == 1:
         w = w[None, :]

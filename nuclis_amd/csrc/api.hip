@@ -88,9 +88,16 @@ int check_matrix(nuq_context *ctx, const nuq_matrix *m, uint64_t *stride) {
 // Whether the vectorised kernels may read this weight range and input
 // (the reference's blockAligned plus its float4 input rule).
 bool vector_aligned(const nuq_matrix *m, uint64_t stride, const void *x) {
+    // ops/matmul.zig:114-123: Q4_K/Q5_K 16, IQ4_XS 8, Q6_K/Q8_0 2
     uintptr_t wp = (uintptr_t)m->bytes;
-    uint64_t need = m->encoding == NUQ_Q4_K ? 16 : 2;
+    uint64_t need = (m->encoding == NUQ_Q4_K || m->encoding == NUQ_Q5_K) ? 16 : m->encoding == NUQ_IQ4_XS ? 8 : 2;
     return wp % need == 0 && stride % need == 0 && ((uintptr_t)x % 16) == 0;
+}
+
+// Encodings with specialised GEMV / multi-token / tile kernels; the others
+// run the generic decode-and-multiply kernels.
+bool specialised(uint32_t encoding) {
+    return encoding == NUQ_Q8_0 || encoding == NUQ_Q4_K || encoding == NUQ_Q6_K;
 }
 
 // Rows per wave of the M=1 GEMV: the number of rows a wave keeps in flight
@@ -144,7 +151,7 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
     if (kernel == NUQ_KERNEL_ROWS && tokens > 8)
         return fail(ctx, NUQ_INVALID_SHAPE, "the multi-token GEMV serves at most 8 tokens");
     const uint32_t f16 = x_dtype == NUQ_F16;
-    const bool aligned = vector_aligned(m, stride, x);
+    const bool aligned = vector_aligned(m, stride, x) && specialised(m->encoding);
     if (ctx->generic_only || kernel == NUQ_KERNEL_GENERIC || !aligned)
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_AUTO) {
@@ -275,7 +282,7 @@ int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out
     if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
     if ((uintptr_t)x % 4 != 0 || (uintptr_t)out % 4 != 0)
         return fail(ctx, NUQ_INVALID_SHAPE, "input and output must be 4-byte aligned");
-    if (ctx->generic_only || !vector_aligned(m, stride, x))
+    if (ctx->generic_only || !vector_aligned(m, stride, x) || !specialised(m->encoding))
         return run_generic(ctx, m, stride, x, 0, m->columns, out, m->rows, 1);
     return run_gemv(ctx, m, stride, x, out);
 }
@@ -293,7 +300,7 @@ int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint6
     if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
     if ((uintptr_t)x % 16 != 0 || in_stride % 4 != 0 || (uintptr_t)out % 4 != 0)
         return fail(ctx, NUQ_INVALID_SHAPE, "input must be float4 aligned (offset and stride)");
-    if (ctx->generic_only || !vector_aligned(m, stride, x))
+    if (ctx->generic_only || !vector_aligned(m, stride, x) || !specialised(m->encoding))
         return run_generic(ctx, m, stride, x, 0, in_stride, out, out_stride, tokens);
     return hip_check(ctx,
                      nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,

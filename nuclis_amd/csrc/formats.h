@@ -6,8 +6,12 @@
 //                 quant/decode.zig:57-63
 //   Q4_K (id 12): [d:f16][dmin:f16][scales:12 B][qs:128 B]     144 B / 256 values
 //                 quant/decode.zig:147-170 (kBlock, fifth_bit false)
+//   Q5_K (id 13): [d:f16][dmin:f16][scales:12 B][qh:32 B][qs:128 B] 176 B / 256
+//                 quant/decode.zig:147-170 (kBlock, fifth_bit true)
 //   Q6_K (id 14): [ql:128 B][qh:64 B][sc:i8 x16][d:f16]        210 B / 256 values
 //                 quant/decode.zig:198-211 (q6Block)
+//   IQ4_XS (id 23): [d:f16][scales_h:u16][scales_l:4 B][qs:128 B] 136 B / 256
+//                 quant/decode.zig:213-228 (iq4XsBlock), values :437
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -26,7 +30,9 @@ __host__ __device__ inline bool layout_of(uint32_t encoding, Layout *l) {
     switch (encoding) {
     case 8: *l = {32, 34}; return true;
     case 12: *l = {256, 144}; return true;
+    case 13: *l = {256, 176}; return true;
     case 14: *l = {256, 210}; return true;
+    case 23: *l = {256, 136}; return true;
     default: return false;
     }
 }
@@ -101,6 +107,44 @@ __device__ __forceinline__ float decode_q4_k(const uint8_t *block, uint32_t i) {
     return scaled - offset;
 }
 
+__device__ __forceinline__ float decode_q5_k(const uint8_t *block, uint32_t i) {
+    float d = half_bits_exact(load_u16_bytes(block));
+    float dmin = half_bits_exact(load_u16_bytes(block + 2));
+    const uint8_t *s = block + 4;
+    uint32_t g = i / 32, c = i % 32;
+    uint32_t scale, minimum;
+    if (g < 4) {
+        scale = s[g] & 63u;
+        minimum = s[g + 4] & 63u;
+    } else {
+        scale = (s[g + 4] & 15u) | ((uint32_t)(s[g - 4] >> 6) << 4);
+        minimum = (uint32_t)(s[g + 4] >> 4) | ((uint32_t)(s[g] >> 6) << 4);
+    }
+    float multiplier = d * (float)scale;
+    float offset = dmin * (float)minimum;
+    uint32_t byte = block[48 + g / 2 * 32 + c];
+    uint32_t q = (g % 2 == 0) ? (byte & 15u) : (byte >> 4);
+    q |= ((uint32_t)(block[16 + c] >> g) & 1u) << 4;  // bit g of high-plane byte c
+    float scaled = multiplier * (float)q;
+    return scaled - offset;
+}
+
+// quant/decode.zig:437
+__constant__ static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                                   1,    13,   25,  38,  53,  69,  89,  113};
+
+__device__ __forceinline__ float decode_iq4_xs(const uint8_t *block, uint32_t i) {
+    float d = half_bits_exact(load_u16_bytes(block));
+    uint32_t high = load_u16_bytes(block + 2);
+    uint32_t g = i / 32, j = i % 32;
+    uint32_t low = (block[4 + g / 2] >> (4 * (g % 2))) & 15u;
+    int scale = (int)(low | (((high >> (2 * g)) & 3u) << 4)) - 32;
+    float multiplier = d * (float)scale;
+    uint32_t byte = block[8 + g * 16 + (j & 15)];
+    uint32_t code = j < 16 ? (byte & 15u) : (byte >> 4);
+    return multiplier * (float)kIq4Values[code];
+}
+
 __device__ __forceinline__ float decode_q6_k(const uint8_t *block, uint32_t i) {
     float d = half_bits_exact(load_u16_bytes(block + 208));
     uint32_t quarter = (i % 128) / 32;
@@ -117,6 +161,8 @@ __device__ __forceinline__ float decode_value(uint32_t encoding, const uint8_t *
     switch (encoding) {
     case 8: return decode_q8_0(block, i);
     case 12: return decode_q4_k(block, i);
+    case 13: return decode_q5_k(block, i);
+    case 23: return decode_iq4_xs(block, i);
     default: return decode_q6_k(block, i);
     }
 }

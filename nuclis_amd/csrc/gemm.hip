@@ -334,7 +334,7 @@ struct WRaw<8> {
     }
 };
 
-constexpr int PF_BM = 256, PF_BN = 256, PF_THREADS = 512, PF_GROUP_M = 4;
+constexpr int PF_BM = 256, PF_BN = 256, PF_GROUP_M = 4;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;

@@ -587,6 +587,19 @@ __device__ __forceinline__ void gemv_rows_any(uint32_t encoding, const uint8_t *
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] += q6k_lane_dot(rowp[r] + (uint64_t)b * 210, h, l, xq, sxq);
         }
+    } else if (encoding != 8) {
+        // Q5_K / IQ4_XS (256-value blocks): exact decode, 4 values per lane per pass
+        Layout l;
+        layout_of(encoding, &l);
+        for (uint32_t c0 = 4 * lane; c0 < nblocks * 256; c0 += 256) {
+            const uint32_t blk = c0 / 256, i = c0 % 256;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint8_t *bp = rowp[r] + (uint64_t)blk * l.bytes;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r] = fmaf(decode_value(encoding, bp, i + e), x[c0 + e], acc[r]);
+            }
+        }
     } else {
         const uint32_t slot = lane >> 2, k = lane & 3;
         for (uint32_t b = slot; b < nblocks; b += 16) {

@@ -1,17 +1,25 @@
-// Host-side weight preparation: F32 rows -> GGUF Q8_0 / Q4_K / Q6_K rows.
+// Host-side weight preparation: F32 rows -> GGUF Q8_0 / Q4_K / Q5_K / Q6_K /
+// IQ4_XS rows.
 //
 // Q8_0 restates nuclis's only encoder, quant/encode.zig:17-36 (q8_0Row):
 // d = f16(max|x| / 127) rounded to nearest even; q = clamp(round(x / d),
 // -127, 127) rounding half away from zero; a zero or non-finite d stores zero
 // codes and a NaN value codes as zero.
 //
-// nuclis has no Q4_K or Q6_K quantizer (encode.zig:1-2); the two below are
+// nuclis has no K-quant or IQ quantizer (encode.zig:1-2); the ones below are
 // this library's own, deterministic and simple (no error search). They write
-// legal blocks in the layouts quant/decode.zig:147-170 and :198-211 read:
+// legal blocks in the layouts quant/decode.zig:147-170, :198-211 and :213-228
+// read:
 //   Q4_K: per 32-value group g, scale s_g = (max - min') / 15 and offset
 //         o_g = -min' with min' = min(min, 0); d = f16(max s_g / 63),
 //         dmin = f16(max o_g / 63); sc_g = round(s_g / d), m_g = round(o_g /
 //         dmin) in 0..63; q = clamp(round((x + dmin*m_g) / (d*sc_g)), 0, 15).
+//   Q5_K: as Q4_K with 32 levels (s_g = (max - min') / 31, q in 0..31); bit
+//         4 of group g's code goes to bit g of high-plane byte c.
+//   IQ4_XS: per 32-value group, s_g = max|x| / 127; d = f16(max s_g / 31);
+//         scale_g = round(s_g / d) in 0..31 (stored +32 as six bits); each
+//         value takes the nearest of the 16 nonlinear code values times
+//         d*scale_g.
 //   Q6_K: per 16-value group, s_g = max|x| / 31; d = f16(max s_g / 127);
 //         sc_g = round(s_g / d) in 0..127; q = clamp(round(x / (d*sc_g)),
 //         -32, 31) + 32 split into a low nibble (ql) and two high bits (qh).
@@ -87,10 +95,14 @@ void q8_0_row(const float *x, uint64_t n, uint8_t *out) {
 
 int clampi(long v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : (int)v); }
 
-void q4_k_row(const float *x, uint64_t n, uint8_t *out) {
+// Q4_K (levels 15, codes at 16) and Q5_K (levels 31, high plane at 16,
+// codes at 48) share the affine group scheme.
+void k_row(bool fifth_bit, const float *x, uint64_t n, uint8_t *out) {
+    const uint64_t bb = fifth_bit ? 176 : 144;
+    const float levels = fifth_bit ? 31.f : 15.f;
     for (uint64_t b = 0; b < n / 256; ++b) {
         const float *v = x + b * 256;
-        uint8_t *blk = out + b * 144;
+        uint8_t *blk = out + b * bb;
         float scale[8], offset[8];
         float max_scale = 0.f, max_offset = 0.f;
         for (int g = 0; g < 8; ++g) {
@@ -100,7 +112,7 @@ void q4_k_row(const float *x, uint64_t n, uint8_t *out) {
                 lo = std::fmin(lo, t);
                 hi = std::fmax(hi, t);
             }
-            scale[g] = (hi - lo) / 15.f;
+            scale[g] = (hi - lo) / levels;
             offset[g] = -lo;
             max_scale = std::fmax(max_scale, scale[g]);
             max_offset = std::fmax(max_offset, offset[g]);
@@ -121,15 +133,58 @@ void q4_k_row(const float *x, uint64_t n, uint8_t *out) {
             s[g + 4] = (uint8_t)((mn[g] & 63) | ((mn[g + 4] >> 4) << 6));
             s[g + 8] = (uint8_t)((sc[g + 4] & 15) | ((mn[g + 4] & 15) << 4));
         }
-        uint8_t *qs = blk + 16;
-        std::memset(qs, 0, 128);
+        uint8_t *qh = blk + 16, *qs = blk + (fifth_bit ? 48 : 16);
+        std::memset(blk + 16, 0, bb - 16);
         for (int g = 0; g < 8; ++g) {
             float mul = d * (float)sc[g], off = dmin * (float)mn[g];
             for (int c = 0; c < 32; ++c) {
-                int q = mul > 0.f ? clampi(std::lround((v[g * 32 + c] + off) / mul), 0, 15) : 0;
-                qs[g / 2 * 32 + c] |= (uint8_t)(g % 2 == 0 ? q : (q << 4));
+                int q = mul > 0.f ? clampi(std::lround((v[g * 32 + c] + off) / mul), 0, (int)levels) : 0;
+                qs[g / 2 * 32 + c] |= (uint8_t)(g % 2 == 0 ? (q & 15) : ((q & 15) << 4));
+                if (fifth_bit) qh[c] |= (uint8_t)(((q >> 4) & 1) << g);
             }
         }
+    }
+}
+
+const int kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+void iq4_xs_row(const float *x, uint64_t n, uint8_t *out) {
+    for (uint64_t b = 0; b < n / 256; ++b) {
+        const float *v = x + b * 256;
+        uint8_t *blk = out + b * 136;
+        float scale[8], max_scale = 0.f;
+        for (int g = 0; g < 8; ++g) {
+            float amax = 0.f;
+            for (int c = 0; c < 32; ++c) amax = std::fmax(amax, std::fabs(v[g * 32 + c]));
+            scale[g] = amax / 127.f;
+            max_scale = std::fmax(max_scale, scale[g]);
+        }
+        uint16_t dbits = f32_to_f16(max_scale / 31.f);
+        float d = f16_to_f32(dbits);
+        std::memset(blk, 0, 136);
+        put16(blk, dbits);
+        uint16_t high = 0;
+        for (int g = 0; g < 8; ++g) {
+            const int si = d > 0.f ? clampi(std::lround(scale[g] / d), 0, 31) : 0;
+            const unsigned stored = (unsigned)(si + 32);
+            blk[4 + g / 2] |= (uint8_t)((stored & 15) << (4 * (g % 2)));
+            high |= (uint16_t)(((stored >> 4) & 3) << (2 * g));
+            const float mul = d * (float)si;
+            for (int j = 0; j < 32; ++j) {
+                int best = 0;
+                float err = INFINITY;
+                for (int c = 0; c < 16; ++c) {
+                    const float e = std::fabs(v[g * 32 + j] - mul * (float)kIq4Values[c]);
+                    if (e < err) {
+                        err = e;
+                        best = c;
+                    }
+                }
+                uint8_t &byte = blk[8 + g * 16 + (j & 15)];
+                byte |= (uint8_t)(j < 16 ? best : (best << 4));
+            }
+        }
+        put16(blk + 2, high);
     }
 }
 
@@ -170,7 +225,9 @@ extern "C" int nuq_quantize_rows(uint32_t encoding, const float *src, uint64_t r
     switch (encoding) {
     case NUQ_Q8_0: elements = 32; bytes = 34; break;
     case NUQ_Q4_K: elements = 256; bytes = 144; break;
+    case NUQ_Q5_K: elements = 256; bytes = 176; break;
     case NUQ_Q6_K: elements = 256; bytes = 210; break;
+    case NUQ_IQ4_XS: elements = 256; bytes = 136; break;
     default: return NUQ_UNSUPPORTED_ENCODING;
     }
     if (!src || !dst) return NUQ_INVALID_ARGUMENT;
@@ -184,9 +241,13 @@ extern "C" int nuq_quantize_rows(uint32_t encoding, const float *src, uint64_t r
         for (uint64_t r = t; r < rows; r += threads) {
             const float *x = src + r * columns;
             uint8_t *o = (uint8_t *)dst + r * row_bytes;
-            if (encoding == NUQ_Q8_0) q8_0_row(x, columns, o);
-            else if (encoding == NUQ_Q4_K) q4_k_row(x, columns, o);
-            else q6_k_row(x, columns, o);
+            switch (encoding) {
+            case NUQ_Q8_0: q8_0_row(x, columns, o); break;
+            case NUQ_Q4_K: k_row(false, x, columns, o); break;
+            case NUQ_Q5_K: k_row(true, x, columns, o); break;
+            case NUQ_IQ4_XS: iq4_xs_row(x, columns, o); break;
+            default: q6_k_row(x, columns, o); break;
+            }
         }
     };
     if (threads == 1) {

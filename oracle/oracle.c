@@ -66,7 +66,9 @@ static int layout(uint32_t encoding, size_t *elements, size_t *bytes) {
     case 1: *elements = 1; *bytes = 2; return 1;
     case 8: *elements = 32; *bytes = 34; return 1;
     case 12: *elements = 256; *bytes = 144; return 1;
+    case 13: *elements = 256; *bytes = 176; return 1;
     case 14: *elements = 256; *bytes = 210; return 1;
+    case 23: *elements = 256; *bytes = 136; return 1;
     default: return 0;
     }
 }
@@ -82,12 +84,14 @@ int orc_validate_row(uint32_t encoding, size_t byte_count, size_t element_count)
 
 static float half_at(const uint8_t *p) { return orc_half_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
 
-/* decode.zig:147-170, Q4_K arm (fifth_bit false). */
-static void q4k_block(const uint8_t *block, float *out) {
+/* decode.zig:147-170, kBlock: Q4_K (fifth_bit 0, codes at 16) and Q5_K
+ * (fifth_bit 1: codes at 48, and byte 16 + c of the high-bit plane gives
+ * bit g of column c as bit 4 of group g's code). */
+static void k_block(int fifth_bit, const uint8_t *block, float *out) {
     float d = half_at(block);
     float dmin = half_at(block + 2);
     const uint8_t *s = block + 4;
-    const uint8_t *low = block + 16;
+    const uint8_t *low = block + (fifth_bit ? 48 : 16);
     for (int g = 0; g < 8; ++g) {
         unsigned scale, minimum;
         if (g < 4) {
@@ -102,6 +106,7 @@ static void q4k_block(const uint8_t *block, float *out) {
         for (int c = 0; c < 32; ++c) {
             uint8_t byte = low[g / 2 * 32 + c];
             unsigned q = (g % 2 == 0) ? (byte & 15u) : (unsigned)(byte >> 4);
+            if (fifth_bit) q |= (unsigned)((block[16 + c] >> g) & 1u) << 4;
             float scaled = multiplier * (float)q;
             out[g * 32 + c] = scaled - offset;
         }
@@ -125,6 +130,28 @@ static void q6k_block(const uint8_t *block, float *out) {
     }
 }
 
+/* decode.zig:437, the IQ4_NL / IQ4_XS nonlinear code values. */
+static const int8_t iq4_values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* decode.zig:213-228, IQ4_XS: [d:f16][scales_h:u16][scales_l:4 B][qs:128 B].
+ * Group g's six-bit scale is nibble g%2 of scales_l[g/2] plus bits 2g..2g+1
+ * of scales_h, biased by -32; qs[16g + j] holds values 32g + j (low nibble)
+ * and 32g + j + 16 (high nibble). */
+static void iq4xs_block(const uint8_t *block, float *out) {
+    float d = half_at(block);
+    unsigned high = (unsigned)block[2] | ((unsigned)block[3] << 8);
+    for (int g = 0; g < 8; ++g) {
+        unsigned low = (block[4 + g / 2] >> (4 * (g % 2))) & 15u;
+        int scale = (int)(low | (((high >> (2 * g)) & 3u) << 4)) - 32;
+        float multiplier = d * (float)scale;
+        for (int j = 0; j < 16; ++j) {
+            uint8_t byte = block[8 + g * 16 + j];
+            out[g * 32 + j] = multiplier * (float)iq4_values[byte & 15];
+            out[g * 32 + j + 16] = multiplier * (float)iq4_values[byte >> 4];
+        }
+    }
+}
+
 int orc_decode_row(uint32_t encoding, const uint8_t *bytes, size_t byte_count, float *out, size_t element_count) {
     int err = orc_validate_row(encoding, byte_count, element_count);
     if (err) return err;
@@ -140,8 +167,10 @@ int orc_decode_row(uint32_t encoding, const uint8_t *bytes, size_t byte_count, f
             for (int j = 0; j < 32; ++j) out[o + j] = scale * (float)(int8_t)block[2 + j];
             break;
         }
-        case 12: q4k_block(block, out + o); break;
+        case 12: k_block(0, block, out + o); break;
+        case 13: k_block(1, block, out + o); break;
         case 14: q6k_block(block, out + o); break;
+        case 23: iq4xs_block(block, out + o); break;
         }
     }
     return ORC_OK;

@@ -13,8 +13,10 @@
  *                        nearest even, overflow to infinity)
  *   orc_validate_row     inference/src/quant/decode.zig:108-120  (validateRow)
  *   orc_decode_row       inference/src/quant/decode.zig:30-106   (row), arms
- *                        0 (F32), 1 (F16), 8 (Q8_0, :57-63), 12 (Q4_K, kBlock
- *                        :147-170) and 14 (Q6_K, q6Block :198-211)
+ *                        0 (F32), 1 (F16), 8 (Q8_0, :57-63), 12 (Q4_K) and
+ *                        13 (Q5_K) (kBlock :147-170), 14 (Q6_K, q6Block
+ *                        :198-211) and 23 (IQ4_XS, iq4XsBlock :213-228 with
+ *                        the iq4_values table :437)
  *   orc_q8_0_row         inference/src/quant/encode.zig:17-36    (q8_0Row)
  *   orc_matvec           inference/src/backends/cpu/root.zig:97-165 (matvec,
  *                        Rows.run, Rows.task)

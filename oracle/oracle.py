@@ -25,7 +25,7 @@ ERROR_NAMES = {
 }
 
 # inference/src/tensor/encoding.zig:29-41
-LAYOUT = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+LAYOUT = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 23: (256, 136)}
 
 
 class OracleError(Exception):

@@ -2,7 +2,8 @@
 nuclis reference holds (data only; nothing of the reference is imported or run).
 
 Source files (MIT, nuclis): inference/src/quant/fixtures/simple.json (Q8_0 row),
-k-affine.json (Q4_K row) and k-signed.json (Q6_K row). They are llama.cpp
+k-affine.json (Q4_K and Q5_K rows), k-signed.json (Q6_K row) and iq.json
+(IQ4_XS row). They are llama.cpp
 7620399f CPU decoder outputs; the reference pins its decoders against them in
 inference/src/quant/decode.zig:587-592 and :706-724. Values are stored as the
 F32 bit patterns so the fixture is exact.
@@ -15,18 +16,19 @@ from pathlib import Path
 
 import numpy as np
 
-WANTED = {"simple.json": 8, "k-affine.json": 12, "k-signed.json": 14}
+WANTED = {"simple.json": (8,), "k-affine.json": (12, 13), "k-signed.json": (14,), "iq.json": (23,)}
 
 
 def main(reference: str) -> None:
     src = Path(reference) / "inference/src/quant/fixtures"
     rows = []
     revision = None
-    for name, encoding in WANTED.items():
+    for name, encodings in WANTED.items():
         data = json.loads((src / name).read_text())
         revision = data["revision"]
         for row in data["rows"]:
-            if row["encoding"] != encoding:
+            encoding = row["encoding"]
+            if encoding not in encodings:
                 continue
             values = np.array([float(v) for v in row["values"]], dtype=np.float32)
             rows.append({

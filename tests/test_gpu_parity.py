@@ -53,7 +53,7 @@ def tame(w, encoding):
     """metal-check.zig:329-345 (tameScales): F16 scales set to 2^-6."""
     n, size = nq.LAYOUT[encoding]
     b = w.reshape(-1, size).copy()
-    positions = {12: (0, 2), 14: (208,), 8: (0,)}[encoding]
+    positions = {12: (0, 2), 13: (0, 2), 14: (208,), 8: (0,), 23: (0,)}[encoding]
     for p in positions:
         b[:, p] = 0x00
         b[:, p + 1] = 0x24
@@ -65,7 +65,10 @@ def quantized(encoding, rows, columns, seed):
 
 
 # ---------------------------------------------------------------- dequant
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+ALL = [8, 12, 13, 14, 23]
+
+
+@pytest.mark.parametrize("encoding", ALL)
 def test_embed_fixture_rows_bit_exact(backend, encoding):
     import torch
     raw, values = fixture_blocks(encoding)
@@ -80,7 +83,8 @@ def test_embed_fixture_rows_bit_exact(backend, encoding):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), values[token * n:(token + 1) * n].view(np.uint32))
 
 
-@pytest.mark.parametrize("encoding,rows,columns", [(8, 96, 4096), (12, 64, 5120), (14, 40, 17408), (12, 35, 17408)])
+@pytest.mark.parametrize("encoding,rows,columns", [(8, 96, 4096), (12, 64, 5120), (14, 40, 17408), (12, 35, 17408),
+                                                   (13, 48, 5120), (23, 40, 5120)])
 def test_dequant_rows_bit_exact_tiled_and_random(backend, encoding, rows, columns):
     import torch
     for w in (tiled(encoding, rows, columns), quantized(encoding, rows, columns, 7)):
@@ -120,6 +124,10 @@ GEMV_SHAPES = [
     (12, 257, 1024),      # one wave set, ragged last workgroup
     (12, 100, 24576),     # 8-block lane groups on the DMA kernel
     (12, 64, 32768),      # x and the rings exceed LDS: register kernel
+    (13, 1024, 5120),     # Q5_K and IQ4_XS
+    (23, 1024, 5120),
+    (13, 35, 1280),
+    (23, 35, 1280),
 ]
 
 
@@ -136,7 +144,7 @@ def test_matvec_matches_oracle(backend, encoding, rows, columns):
                 extra=xq_mass(encoding, w, rows, columns, x)[0] if encoding in INT_GEMV else 0.0)
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", ALL)
 def test_matvec_tiled_fixture_blocks_and_basis_columns(backend, encoding):
     """Fixture blocks (extreme real scales) tiled into 35 x 1280; plus one-hot
     inputs that select decoded columns (cpu/root.zig:240-272)."""
@@ -161,7 +169,7 @@ def test_matvec_tiled_fixture_blocks_and_basis_columns(backend, encoding):
         assert np.all(np.abs(got - dec[:, column]) <= 1e-5 * np.abs(dec[:, column])), column
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", ALL)
 def test_generic_control_and_misaligned_weights(backend, encoding):
     import torch
     rows, columns = 48, 1024
@@ -206,7 +214,7 @@ def test_matvec_refusals_leave_output_untouched(backend):
 
 # ---------------------------------------------------------------- multi-token
 @pytest.mark.parametrize("encoding,rows,columns", [(12, 2048, 5120), (14, 1024, 5120), (8, 512, 4096),
-                                                   (12, 512, 17408)])
+                                                   (12, 512, 17408), (13, 512, 5120), (23, 512, 5120)])
 @pytest.mark.parametrize("tokens", [2, 3, 5, 8])
 def test_matvec_rows_matches_oracle(backend, encoding, rows, columns, tokens):
     import torch
@@ -231,6 +239,9 @@ TILE_CASES = [
     (14, 520, 5120, 300), (8, 264, 4096, 257), (12, 512, 1280, 512),
     # 260 prefill tiles: 256 whole tiles, then 4 tiles split along K
     (12, 33064, 1024, 257),
+    # Q5_K and IQ4_XS at verify, tile and prefill token counts
+    (13, 512, 5120, 8), (23, 512, 5120, 8), (13, 256, 1280, 37), (23, 256, 1280, 37),
+    (13, 520, 2048, 300), (23, 520, 2048, 300),
 ]
 
 
@@ -275,7 +286,7 @@ def test_prefill_split_k_is_deterministic(backend, encoding, rows, columns, toke
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", ALL)
 def test_tile_tamed_fixture_blocks(backend, encoding):
     """metal-check.zig:4355-4436: fixture blocks with tamed scales, 40 rows,
     token counts 37/20/16/9/8/5/1, against the oracle."""
@@ -323,17 +334,11 @@ def test_matmul_refusals(backend):
 # ---------------------------------------------------------------- segments / argmax
 def test_segments_plain_and_silu_pair(backend):
     import torch
+    segments_plain(backend, [(12, 1024), (12, 512), (14, 256), (8, 128)])
+    segments_plain(backend, [(13, 512), (23, 256), (12, 256)])
     columns = 5120
-    shapes = [(12, 1024), (12, 512), (14, 256), (8, 128)]
-    ws = [quantized(e, r, columns, 40 + i) for i, (e, r) in enumerate(shapes)]
     x = gaussian(41, columns)
     xg = to_gpu(x)
-    outs = [torch.full((r,), np.nan, device="cuda") for _, r in shapes]
-    segs = [(nq.Matrix(e, r, columns, to_gpu(w)), o) for (e, r), w, o in zip(shapes, ws, outs)]
-    backend.matvec_segments(segs, xg, nq.SEGMENT_PLAIN)
-    backend.sync()
-    for (e, r), w, o in zip(shapes, ws, outs):
-        check_close(o.cpu().numpy(), orc.matvec(e, r, columns, w, x), mass(e, w, r, columns, x)[0], F32_K, "segment")
     # gate/up pair: out = silu(gate x) * (up x)
     gate, up = quantized(12, 1024, columns, 50), quantized(12, 1024, columns, 51)
     pair_out = torch.full((1024,), np.nan, device="cuda")
@@ -348,6 +353,20 @@ def test_segments_plain_and_silu_pair(backend):
     # first-order propagation of the two F32 bounds through silu(g)*u (|silu'| <= 1.1)
     bound = 1.1 * np.abs(u) * (F32_K * mg + 1e-6) + np.abs(g) * (F32_K * mu + 1e-6) + 1e-6
     assert np.all(np.abs(got - want) <= bound)
+
+
+def segments_plain(backend, shapes):
+    import torch
+    columns = 5120
+    ws = [quantized(e, r, columns, 40 + i) for i, (e, r) in enumerate(shapes)]
+    x = gaussian(41, columns)
+    xg = to_gpu(x)
+    outs = [torch.full((r,), np.nan, device="cuda") for _, r in shapes]
+    segs = [(nq.Matrix(e, r, columns, to_gpu(w)), o) for (e, r), w, o in zip(shapes, ws, outs)]
+    backend.matvec_segments(segs, xg, nq.SEGMENT_PLAIN)
+    backend.sync()
+    for (e, r), w, o in zip(shapes, ws, outs):
+        check_close(o.cpu().numpy(), orc.matvec(e, r, columns, w, x), mass(e, w, r, columns, x)[0], F32_K, "segment")
 
 
 def test_argmax_first_maximum(backend):

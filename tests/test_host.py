@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", [8, 12, 13, 14, 23])
 def test_validate_row_matches_oracle(encoding):
     n, size = nq.LAYOUT[encoding]
     cases = [(0, 0), (size, n), (size - 1, n), (size + 1, n), (size, 2 * n), (2 * size, n), (size, n - 1),
@@ -79,6 +79,40 @@ def test_k_quantizers_round_trip(encoding, tol):
     assert np.all(err.reshape(16, -1, group) <= step[..., None] * tol + 1e-7)
     rel = np.linalg.norm(back - w) / np.linalg.norm(w)
     assert rel < (0.1 if encoding == 12 else 0.03)
+
+
+def test_q5_k_quantizer_round_trip():
+    """Own Q5_K quantizer: within a small fraction of the 31-level group step."""
+    w = gaussian(4, (16, 1024), 0.02)
+    q = nq.quantize(13, w)
+    assert q.shape == (16, nq.row_bytes(13, 1024))
+    back = orc.decode_matrix(13, q, 16, 1024)
+    spread = w.reshape(16, -1, 32)
+    step = (spread.max(-1) - np.minimum(spread.min(-1), 0)) / 31
+    assert np.all(np.abs(back - w).reshape(16, -1, 32) <= step[..., None] * 0.6 + 1e-7)
+    assert np.linalg.norm(back - w) / np.linalg.norm(w) < 0.05
+
+
+def test_iq4_xs_quantizer_round_trip():
+    """Own IQ4_XS quantizer: every value is the nearest of the 16 code values
+    at its group's stored scale, and the row error is that of a 4-bit code."""
+    w = gaussian(5, (16, 1024), 0.02)
+    q = nq.quantize(23, w)
+    assert q.shape == (16, nq.row_bytes(23, 1024))
+    back = orc.decode_matrix(23, q, 16, 1024)
+    table = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+    blocks = q.reshape(-1, 136)
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    high = blocks[:, 2].astype(np.int32) | (blocks[:, 3].astype(np.int32) << 8)
+    for b in range(blocks.shape[0]):
+        for g in range(8):
+            low = (blocks[b, 4 + g // 2] >> (4 * (g % 2))) & 15
+            mul = d[b] * ((low | (((high[b] >> (2 * g)) & 3) << 4)) - 32)
+            vals = w.reshape(-1, 256)[b, g * 32:(g + 1) * 32]
+            best = np.min(np.abs(vals[:, None] - mul * table[None, :]), axis=1)
+            got = np.abs(vals - back.reshape(-1, 256)[b, g * 32:(g + 1) * 32])
+            assert np.all(got <= best + 1e-9)
+    assert np.linalg.norm(back - w) / np.linalg.norm(w) < 0.12
 
 
 def test_quantizer_refusals():

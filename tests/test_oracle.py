@@ -5,7 +5,7 @@ Sources of truth, none of them a retyping of the oracle's formulas:
     (inference/src/quant/fixtures/*.json -> tests/golden/decoder_fixtures.json),
     decoded from an unaligned copy as decode.zig:706-724 does;
   * the reference's known-answer tests (decode.zig:455-473, :566-585,
-    :692-704, :754-764; encode.zig:40-71; cpu/root.zig:171-298);
+    :692-704, :726-737, :754-779; encode.zig:40-71; cpu/root.zig:171-298);
   * numpy's IEEE float16 for both half conversions, exhaustively/randomly;
   * brute-force F64 sums for matvec.
 """
@@ -31,7 +31,10 @@ def test_fixture_revision():
     assert GOLDEN["revision"] == "7620399f58aebfd2196b74021f9581bcf7218cb9"
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+ALL = [8, 12, 13, 14, 23]
+
+
+@pytest.mark.parametrize("encoding", ALL)
 def test_decoders_match_llama_cpp_fixtures_from_unaligned_storage(encoding):
     raw, values = fixture(encoding)
     buf = np.zeros(len(raw) + 1, np.uint8)
@@ -106,6 +109,31 @@ def test_q4_k_six_bit_coefficients_for_every_group():
     assert np.array_equal(orc.decode_row(12, b, 256), want)
 
 
+def test_q5_k_high_bit_plane_selects_group_and_column():
+    # decode.zig:766-779: d = 1, group scales 1 and minima 0; codes 3 (low
+    # nibble) and 10 (high); high-plane byte c has bit c % 8 set, so value i
+    # gains 16 exactly when column i % 32 has bit (i / 32) set
+    b = np.zeros(176, np.uint8)
+    b[1] = 0x3C
+    b[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    b[48:] = 0xA3
+    b[16:48] = [1 << (c % 8) for c in range(32)]
+    want = np.array([(3 if (i // 32) % 2 == 0 else 10) + (16 if i % 8 == i // 32 else 0) for i in range(256)],
+                    np.float32)
+    assert np.array_equal(orc.decode_row(13, b, 256), want)
+
+
+def test_iq4_xs_six_bit_signed_scales_and_half_row_order():
+    # decode.zig:726-737: d = 0.5; packed scale bytes give the eight signed
+    # group scales below; every code byte 0xF0 puts table entry 0 (-127) in the
+    # first 16 values of a group and entry 15 (113) in the last 16
+    b = np.full(136, 0xF0, np.uint8)
+    b[0:8] = [0, 0x38, 0xE4, 0xE4, 0x10, 0x32, 0x54, 0xFE]
+    scales = [-32, -15, 2, 19, -28, -11, 14, 31]
+    want = np.array([0.5 * scales[i // 32] * (-127 if i % 32 < 16 else 113) for i in range(256)], np.float32)
+    assert np.array_equal(orc.decode_row(23, b, 256), want)
+
+
 def test_q4_k_subnormal_scales_stay_exact():
     # metal-check.zig:4632: subnormal F16 scales must not flush to zero
     b = np.zeros(144, np.uint8)
@@ -118,7 +146,7 @@ def test_q4_k_subnormal_scales_stay_exact():
     assert got[0] == lo and got[0] != 0
 
 
-@pytest.mark.parametrize("encoding", [0, 1, 8, 12, 14])
+@pytest.mark.parametrize("encoding", [0, 1] + ALL)
 def test_invalid_rows_are_refused(encoding):
     # decode.zig:566-585
     n, size = orc.LAYOUT[encoding]
@@ -229,7 +257,7 @@ def test_matvec_refusals_leave_output_untouched():
         orc.matvec(999, 2, 32, b, x)
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", ALL)
 def test_basis_vectors_select_fixture_columns(encoding):
     # cpu/root.zig:240-272
     raw, values = fixture(encoding)
@@ -256,7 +284,7 @@ def test_matvec_split_across_tasks_is_bit_identical():
         assert np.array_equal(orc.matvec(8, rows, columns, b, x, threads=t).view(np.uint32), serial.view(np.uint32))
 
 
-@pytest.mark.parametrize("encoding", [8, 12, 14])
+@pytest.mark.parametrize("encoding", ALL)
 def test_matvec_equals_f64_sum_of_decoded_rows(encoding):
     """Closed form: y = f32(sum_c f64(w) f64(x)), checked with math.fsum
     (exactly rounded) so only the reference's one final rounding differs."""
