@@ -94,8 +94,9 @@ bool vector_aligned(const nuq_matrix *m, uint64_t stride, const void *x) {
     return wp % need == 0 && stride % need == 0 && ((uintptr_t)x % 16) == 0;
 }
 
-// Encodings with specialised GEMV / multi-token / tile kernels; the others
-// run the generic decode-and-multiply kernels.
+// Encodings with specialised M=1 GEMV and multi-token GEMV kernels; the MFMA
+// tiles take every supported encoding. The others run the generic
+// decode-and-multiply kernels.
 bool specialised(uint32_t encoding) {
     return encoding == NUQ_Q8_0 || encoding == NUQ_Q4_K || encoding == NUQ_Q6_K;
 }
@@ -151,13 +152,15 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
     if (kernel == NUQ_KERNEL_ROWS && tokens > 8)
         return fail(ctx, NUQ_INVALID_SHAPE, "the multi-token GEMV serves at most 8 tokens");
     const uint32_t f16 = x_dtype == NUQ_F16;
-    const bool aligned = vector_aligned(m, stride, x) && specialised(m->encoding);
+    const bool aligned = vector_aligned(m, stride, x);
     if (ctx->generic_only || kernel == NUQ_KERNEL_GENERIC || !aligned)
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_AUTO) {
-        if (tokens == 1 && !f16) return run_gemv(ctx, m, stride, (const float *)x, out);
-        kernel = tokens <= 3 ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
+        if (tokens == 1 && !f16 && specialised(m->encoding)) return run_gemv(ctx, m, stride, (const float *)x, out);
+        kernel = tokens <= 3 && specialised(m->encoding) ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
     }
+    if (kernel == NUQ_KERNEL_ROWS && !specialised(m->encoding))
+        return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_ROWS)
         return hip_check(ctx,
                          nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,

@@ -79,6 +79,52 @@ __device__ __forceinline__ void dequant_step(const uint8_t *__restrict__ row, ui
             for (int e = 0; e < 4; ++e)
                 out[part * 32 + 4 * k + e] = (_Float16)(mul * (float)((int)((u >> (8 * e)) & 0xffu) - 32));
         }
+    } else if constexpr (ENC == 13) {
+        // Q5_K: as Q4_K, with bit 2p (low-nibble group) or 2p+1 of high-plane
+        // byte c as bit 4 of column c's code
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 176;
+        const uint32_t p = ks & 3;
+        uint4 hdr = *(const uint4 *)blk;
+        uint4 qh = *(const uint4 *)(blk + 16 + part * 16);
+        uint4 qs = *(const uint4 *)(blk + 48 + p * 32 + part * 16);
+        float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * p, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+        q4k_scale_min(2 * p + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+        float mul0 = d * (float)sc0, off0 = dmin * (float)m0;
+        float mul1 = d * (float)sc1, off1 = dmin * (float)m1;
+        const uint32_t words[4] = {qs.x, qs.y, qs.z, qs.w}, highs[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = (words[k] & 0x0f0f0f0fu) | (((highs[k] >> (2 * p)) & 0x01010101u) << 4);
+            const uint32_t hi = ((words[k] >> 4) & 0x0f0f0f0fu) | (((highs[k] >> (2 * p + 1)) & 0x01010101u) << 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float a = mul0 * (float)((lo >> (8 * e)) & 0xffu);
+                float b = mul1 * (float)((hi >> (8 * e)) & 0xffu);
+                out[part * 16 + 4 * k + e] = (_Float16)(a - off0);
+                out[32 + part * 16 + 4 * k + e] = (_Float16)(b - off1);
+            }
+        }
+    } else if constexpr (ENC == 23) {
+        // IQ4_XS: this thread owns group 2p + part (32 values)
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 136;
+        const uint32_t g = 2 * (ks & 3) + part;
+        const uint2 hdr = *(const uint2 *)blk;
+        const uint32_t low = (hdr.y >> (8 * (g / 2) + 4 * (g % 2))) & 15u;
+        const int sc = (int)(low | (((hdr.x >> (16 + 2 * g)) & 3u) << 4)) - 32;
+        const float mul = half_bits(hdr.x & 0xffffu) * (float)sc;
+        const uint2 q01 = *(const uint2 *)(blk + 8 + 16 * g), q23 = *(const uint2 *)(blk + 16 + 16 * g);
+        const uint32_t words[4] = {q01.x, q01.y, q23.x, q23.y};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t tl = iq4_lookup(words[k] & 0x0f0f0f0fu), th = iq4_lookup((words[k] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                out[part * 32 + 4 * k + e] = (_Float16)(mul * (float)(int8_t)((tl >> (8 * e)) & 0xffu));
+                out[part * 32 + 16 + 4 * k + e] = (_Float16)(mul * (float)(int8_t)((th >> (8 * e)) & 0xffu));
+            }
+        }
     } else {
         const uint8_t *blk = row + (uint64_t)(2 * ks + part) * 34;
         float d = half_bits(load_u16_bytes(blk));
@@ -316,6 +362,86 @@ struct WRaw<14> {
     }
 };
 template <>
+struct WRaw<13> {
+    static constexpr uint32_t MIN_LOADS = 3;
+    uint4 hdr, qh, qs;
+    uint32_t p2;  // 2 * pair: the high-plane bit of the low-nibble group
+    float mul0, off0, mul1, off1;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 176;
+        hdr = *(const uint4 *)blk;
+        qh = *(const uint4 *)(blk + 16 + part * 16);
+        qs = *(const uint4 *)(blk + 48 + (ks & 3) * 32 + part * 16);
+    }
+    __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
+        if (c == 0) {
+            const uint32_t p = ks & 3;
+            const float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scale_min(2 * p, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+            q4k_scale_min(2 * p + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+            mul0 = d * (float)sc0;
+            off0 = dmin * (float)m0;
+            mul1 = d * (float)sc1;
+            off1 = dmin * (float)m1;
+            p2 = 2 * p;
+        }
+        const uint32_t word = c == 0 ? qs.x : c == 1 ? qs.y : c == 2 ? qs.z : qs.w;
+        const uint32_t high = c == 0 ? qh.x : c == 1 ? qh.y : c == 2 ? qh.z : qh.w;
+        const uint32_t lo = (word & 0x0f0f0f0fu) | (((high >> p2) & 0x01010101u) << 4);
+        const uint32_t hi = ((word >> 4) & 0x0f0f0f0fu) | (((high >> (p2 + 1)) & 0x01010101u) << 4);
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        half4 l, h;
+        l[0] = (_Float16)fmaf(mul0, ubyte_f<0>(lo), -off0);
+        l[1] = (_Float16)fmaf(mul0, ubyte_f<1>(lo), -off0);
+        l[2] = (_Float16)fmaf(mul0, ubyte_f<2>(lo), -off0);
+        l[3] = (_Float16)fmaf(mul0, ubyte_f<3>(lo), -off0);
+        h[0] = (_Float16)fmaf(mul1, ubyte_f<0>(hi), -off1);
+        h[1] = (_Float16)fmaf(mul1, ubyte_f<1>(hi), -off1);
+        h[2] = (_Float16)fmaf(mul1, ubyte_f<2>(hi), -off1);
+        h[3] = (_Float16)fmaf(mul1, ubyte_f<3>(hi), -off1);
+        *(half4 *)(out + part * 16 + 4 * c) = l;
+        *(half4 *)(out + 32 + part * 16 + 4 * c) = h;
+    }
+};
+template <>
+struct WRaw<23> {
+    static constexpr uint32_t MIN_LOADS = 3;
+    uint2 hdr, q01, q23;  // d, scales_h, scales_l; the group's 16 code bytes
+    float mul;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 136;
+        const uint32_t g = 2 * (ks & 3) + part;
+        hdr = *(const uint2 *)blk;
+        q01 = *(const uint2 *)(blk + 8 + 16 * g);
+        q23 = *(const uint2 *)(blk + 16 + 16 * g);
+    }
+    // this thread owns group 2(ks&3) + part: chunk c = byte dword c, values
+    // 4c..4c+3 (low nibbles) and 16+4c.. (high nibbles)
+    __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
+        if (c == 0) {
+            const uint32_t g = 2 * (ks & 3) + part;
+            const uint32_t low = (hdr.y >> (8 * (g / 2) + 4 * (g % 2))) & 15u;
+            const int sc = (int)(low | (((hdr.x >> (16 + 2 * g)) & 3u) << 4)) - 32;
+            mul = half_bits(hdr.x & 0xffffu) * (float)sc;
+        }
+        const uint32_t word = c == 0 ? q01.x : c == 1 ? q01.y : c == 2 ? q23.x : q23.y;
+        const uint32_t tl = iq4_lookup(word & 0x0f0f0f0fu), th = iq4_lookup((word >> 4) & 0x0f0f0f0fu);
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        half4 l, h;
+        l[0] = (_Float16)(mul * sbyte_f<0>(tl));
+        l[1] = (_Float16)(mul * sbyte_f<1>(tl));
+        l[2] = (_Float16)(mul * sbyte_f<2>(tl));
+        l[3] = (_Float16)(mul * sbyte_f<3>(tl));
+        h[0] = (_Float16)(mul * sbyte_f<0>(th));
+        h[1] = (_Float16)(mul * sbyte_f<1>(th));
+        h[2] = (_Float16)(mul * sbyte_f<2>(th));
+        h[3] = (_Float16)(mul * sbyte_f<3>(th));
+        *(half4 *)(out + part * 32 + 4 * c) = l;
+        *(half4 *)(out + part * 32 + 16 + 4 * c) = h;
+    }
+};
+template <>
 struct WRaw<8> {
     uint32_t q[8];
     uint32_t d16;
@@ -416,7 +542,7 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
     if (split_k) {
         tile = full + (blockIdx.x - full) % tail;
         split = (blockIdx.x - full) / tail;
-        constexpr uint32_t BLOCK256 = ENC == 12 ? 144 : ENC == 14 ? 210 : 272;  // bytes per 256 columns
+        constexpr uint32_t BLOCK256 = ENC == 12 ? 144 : ENC == 13 ? 176 : ENC == 14 ? 210 : ENC == 23 ? 136 : 272;  // bytes per 256 columns
         const uint32_t nb = columns / 256;
         const uint32_t b0 = split * nb / splits, b1 = (split + 1) * nb / splits;
         w += (uint64_t)b0 * BLOCK256;
@@ -750,6 +876,73 @@ struct VLane<14> {
 };
 
 template <>
+struct VLane<13> {
+    static constexpr uint32_t BLOCK_BYTES = 176, BLOCK_VALUES = 256;
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return 32 * (2 * h + (c >> 2)) + 8 * (c & 3); }
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&a)[8]) {
+        const uint4 hdr = *(const uint4 *)blk;
+        const uint4 h0 = *(const uint4 *)(blk + 16), h1 = *(const uint4 *)(blk + 32);
+        const uint4 q0 = *(const uint4 *)(blk + 48 + 32 * h), q1 = *(const uint4 *)(blk + 64 + 32 * h);
+        const float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * h, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+        q4k_scale_min(2 * h + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+        const float mul0 = d * (float)sc0, off0 = dmin * (float)m0;
+        const float mul1 = d * (float)sc1, off1 = dmin * (float)m1;
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // chunk c: columns 8c..8c+7 of group 2h (low nibbles), c+4: group 2h+1
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t wd = w[2 * c + k], hd = hb[2 * c + k];
+                const uint32_t lo = (wd & 0x0f0f0f0fu) | (((hd >> (2 * h)) & 0x01010101u) << 4);
+                const uint32_t hi = ((wd >> 4) & 0x0f0f0f0fu) | (((hd >> (2 * h + 1)) & 0x01010101u) << 4);
+                a[c][4 * k + 0] = (_Float16)fmaf(mul0, ubyte_f<0>(lo), -off0);
+                a[c][4 * k + 1] = (_Float16)fmaf(mul0, ubyte_f<1>(lo), -off0);
+                a[c][4 * k + 2] = (_Float16)fmaf(mul0, ubyte_f<2>(lo), -off0);
+                a[c][4 * k + 3] = (_Float16)fmaf(mul0, ubyte_f<3>(lo), -off0);
+                a[c + 4][4 * k + 0] = (_Float16)fmaf(mul1, ubyte_f<0>(hi), -off1);
+                a[c + 4][4 * k + 1] = (_Float16)fmaf(mul1, ubyte_f<1>(hi), -off1);
+                a[c + 4][4 * k + 2] = (_Float16)fmaf(mul1, ubyte_f<2>(hi), -off1);
+                a[c + 4][4 * k + 3] = (_Float16)fmaf(mul1, ubyte_f<3>(hi), -off1);
+            }
+        }
+    }
+};
+
+template <>
+struct VLane<23> {
+    static constexpr uint32_t BLOCK_BYTES = 136, BLOCK_VALUES = 256;
+    // quarter h = groups 2h, 2h+1; chunk c of group 2h + c/4: values
+    // 8*(c%4)..+8, i.e. low nibbles of bytes 0-7 / 8-15, then high nibbles
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return 32 * (2 * h + (c >> 2)) + 8 * (c & 3); }
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&a)[8]) {
+        const uint2 hdr = *(const uint2 *)blk;
+        const float d = half_bits(hdr.x & 0xffffu);
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+            const uint32_t g = 2 * h + gg;
+            const uint32_t low = (hdr.y >> (8 * (g / 2) + 4 * (g % 2))) & 15u;
+            const int sc = (int)(low | (((hdr.x >> (16 + 2 * g)) & 3u) << 4)) - 32;
+            const float mul = d * (float)sc;
+            const uint2 qa = *(const uint2 *)(blk + 8 + 16 * g), qb = *(const uint2 *)(blk + 16 + 16 * g);
+            const uint32_t wd[4] = {qa.x, qa.y, qb.x, qb.y};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t tl = iq4_lookup(wd[k] & 0x0f0f0f0fu), th = iq4_lookup((wd[k] >> 4) & 0x0f0f0f0fu);
+                // bytes 4k..4k+3: chunk k/2 (low) and 2 + k/2 (high), elements 4*(k&1)..
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a[4 * gg + (k >> 1)][4 * (k & 1) + e] = (_Float16)(mul * (float)(int8_t)((tl >> (8 * e)) & 0xffu));
+                    a[4 * gg + 2 + (k >> 1)][4 * (k & 1) + e] = (_Float16)(mul * (float)(int8_t)((th >> (8 * e)) & 0xffu));
+                }
+            }
+        }
+    }
+};
+
+template <>
 struct VLane<8> {
     // a "block" here is 8 Q8_0 blocks (256 columns); quarter h = 32-blocks 2h, 2h+1
     static constexpr uint32_t BLOCK_BYTES = 8 * 34, BLOCK_VALUES = 256;
@@ -859,7 +1052,9 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
     if (tokens <= 16 && columns % 256 == 0) {
         switch (encoding) {
         case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        case 13: return launch_verify_enc<13>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
         case 14: return launch_verify_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        case 23: return launch_verify_enc<23>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
         default: return launch_verify_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
         }
     }
@@ -868,13 +1063,17 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
         const uint32_t cus = compute_units();
         switch (encoding) {
         case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
+        case 13: return launch_prefill<13>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
         case 14: return launch_prefill<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
+        case 23: return launch_prefill<23>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
         default: return launch_prefill<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);
         }
     }
     switch (encoding) {
     case 12: return launch_tile_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+    case 13: return launch_tile_enc<13>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
     case 14: return launch_tile_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+    case 23: return launch_tile_enc<23>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
     default: return launch_tile_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
     }
 }
