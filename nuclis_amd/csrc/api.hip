@@ -94,8 +94,8 @@ bool vector_aligned(const nuq_matrix *m, uint64_t stride, const void *x) {
     return wp % need == 0 && stride % need == 0 && ((uintptr_t)x % 16) == 0;
 }
 
-// Encodings with specialised M=1 GEMV and multi-token GEMV kernels; the MFMA
-// tiles take every supported encoding. The others run the generic
+// Encodings with specialised multi-token GEMV kernels; the M=1 GEMV and the
+// MFMA tiles take every supported encoding. The others run the generic
 // decode-and-multiply kernels.
 bool specialised(uint32_t encoding) {
     return encoding == NUQ_Q8_0 || encoding == NUQ_Q4_K || encoding == NUQ_Q6_K;
@@ -112,6 +112,16 @@ int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
 // The decode GEMV: Q4_K on the integer-dot K-split kernel, the other
 // encodings on the row-per-wave kernels.
 int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, float *out) {
+    if (m->encoding == NUQ_Q5_K || m->encoding == NUQ_IQ4_XS) {
+        hipError_t e = nuq::launch_gemv_dma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                            (uint32_t)m->rows, (uint32_t)m->columns, x, out);
+        if (e != hipErrorInvalidValue) return hip_check(ctx, e, "gemv launch");
+        return hip_check(ctx,
+                         nuq::launch_generic(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                             (uint32_t)m->rows, (uint32_t)m->columns, x, 0, m->columns, out, m->rows,
+                                             1),
+                         "generic kernel launch");
+    }
     if (m->encoding == NUQ_Q4_K) {
         const int config = 0;  // DMA kernel, two ring slots; register kernel when LDS is short
         hipError_t e = nuq::launch_gemv_q4k_int(ctx->stream, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
@@ -156,7 +166,7 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
     if (ctx->generic_only || kernel == NUQ_KERNEL_GENERIC || !aligned)
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_AUTO) {
-        if (tokens == 1 && !f16 && specialised(m->encoding)) return run_gemv(ctx, m, stride, (const float *)x, out);
+        if (tokens == 1 && !f16) return run_gemv(ctx, m, stride, (const float *)x, out);
         kernel = tokens <= 3 && specialised(m->encoding) ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
     }
     if (kernel == NUQ_KERNEL_ROWS && !specialised(m->encoding))
@@ -285,8 +295,7 @@ int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out
     if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
     if ((uintptr_t)x % 4 != 0 || (uintptr_t)out % 4 != 0)
         return fail(ctx, NUQ_INVALID_SHAPE, "input and output must be 4-byte aligned");
-    if (ctx->generic_only || !vector_aligned(m, stride, x) || !specialised(m->encoding))
-        return run_generic(ctx, m, stride, x, 0, m->columns, out, m->rows, 1);
+    if (ctx->generic_only || !vector_aligned(m, stride, x)) return run_generic(ctx, m, stride, x, 0, m->columns, out, m->rows, 1);
     return run_gemv(ctx, m, stride, x, out);
 }
 

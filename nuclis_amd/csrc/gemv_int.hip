@@ -371,41 +371,148 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     }
 }
 
-// DMA variant (R = 1). Instead of each lane loading its header and two
-// 16-byte code chunks straight from HBM (three scattered loads that touch
-// every cache line of the step about three times), each wave copies the
-// step's bytes -- GROUPS rows x SLOTS blocks, 144 contiguous 16-byte chunks
-// per step whatever SLOTS is -- into a private LDS ring with three
-// global_load_lds_dwordx4 (lane i of instruction n moves chunk 64n + i), and
-// the lanes then read their header and codes from LDS. Waves never read
+// DMA variant (R = 1), for Q4_K, Q5_K and IQ4_XS. Instead of each lane
+// loading its header and code chunks straight from HBM (scattered loads that
+// touch every cache line of the step about three times), each wave copies
+// the step's bytes -- GROUPS rows x SLOTS blocks, as many contiguous 16-byte
+// chunks as a block has bytes (144, 176, 136) whatever SLOTS is -- into a
+// private LDS ring with three global_load_lds_dwordx4 (lane i of
+// instruction n moves chunk 64n + i), and the lanes then read their bytes
+// from LDS. Waves never read
 // another wave's ring, so only the wave's own vmcnt orders DMA and reads.
-constexpr uint32_t GD_STEP_CHUNKS = 144, GD_DMA_INSTRS = 3, GD_SLOT_BYTES = GD_DMA_INSTRS * 64 * 16;
+constexpr uint32_t GD_DMA_INSTRS = 3, GD_SLOT_BYTES = GD_DMA_INSTRS * 64 * 16;
 
 typedef __attribute__((address_space(3))) void gd_lds_void_t;
 typedef __attribute__((address_space(3))) uint8_t gd_lds_u8_t;
 
-// Reads a lane's header (16 bytes at p) and codes (32 bytes at p + qoff)
-// from its wave's ring once at most VM younger copies are outstanding, and
-// waits for the reads. Written as one asm block because the compiler cannot
-// tell ring slots apart and would otherwise wait for every copy in flight.
-template <int VM>
-__device__ __forceinline__ void ring_read(const uint8_t *p, uint32_t qoff, uint4 &h, uint4 &q0, uint4 &q1) {
-    const uint32_t a = (uint32_t)(uintptr_t)(const gd_lds_u8_t *)p;
-    const uint32_t b = a + qoff;
-    u32x4_t vh, v0, v1;
-    asm volatile(
-        "s_waitcnt vmcnt(%3)\n\t"
-        "ds_read_b128 %0, %4\n\t"
-        "ds_read_b128 %1, %5\n\t"
-        "ds_read_b128 %2, %5 offset:16\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(vh), "=&v"(v0), "=&v"(v1)
-        : "n"(VM), "v"(a), "v"(b)
-        : "memory");
-    h = make_uint4(vh.x, vh.y, vh.z, vh.w);
-    q0 = make_uint4(v0.x, v0.y, v0.z, v0.w);
-    q1 = make_uint4(v1.x, v1.y, v1.z, v1.w);
-}
+// Per-encoding pieces of the DMA kernel. `read<VM>` fetches a lane's bytes
+// of one block from its wave's ring once at most VM younger copies are
+// outstanding, and waits for the reads: one asm block, because the compiler
+// cannot tell ring slots apart and would otherwise wait for every copy in
+// flight. `dot` is the lane's contribution: pair j = groups 2j (x slice A)
+// and 2j+1 (slice B) of the block.
+__device__ __forceinline__ uint32_t lds_u8_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(const gd_lds_u8_t *)p; }
+
+template <uint32_t ENC>
+struct GdEnc;
+
+template <>
+struct GdEnc<12> {  // Q4_K: header + the pair's 32 code bytes
+    static constexpr uint32_t BYTES = 144;
+    u32x4_t h, q0, q1;
+    template <int VM>
+    __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
+        const uint32_t a = lds_u8_addr(blk), b = a + 16 + 32 * j;
+        asm volatile(
+            "s_waitcnt vmcnt(%3)\n\t"
+            "ds_read_b128 %0, %4\n\t"
+            "ds_read_b128 %1, %5\n\t"
+            "ds_read_b128 %2, %5 offset:16\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(h), "=&v"(q0), "=&v"(q1)
+            : "n"(VM), "v"(a), "v"(b)
+            : "memory");
+    }
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t shift,
+                                         bool direct) const {
+        return q4k_lane(make_uint4(h.x, h.y, h.z, h.w), make_uint4(q0.x, q0.y, q0.z, q0.w),
+                        make_uint4(q1.x, q1.y, q1.z, q1.w), A, B, shift, direct);
+    }
+};
+
+template <>
+struct GdEnc<13> {  // Q5_K: header, the 32 high-plane bytes, the pair's 32 code bytes
+    static constexpr uint32_t BYTES = 176;
+    u32x4_t h, qh0, qh1, q0, q1;
+    template <int VM>
+    __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
+        const uint32_t a = lds_u8_addr(blk), b = a + 48 + 32 * j;
+        asm volatile(
+            "s_waitcnt vmcnt(%5)\n\t"
+            "ds_read_b128 %0, %6\n\t"
+            "ds_read_b128 %1, %6 offset:16\n\t"
+            "ds_read_b128 %2, %6 offset:32\n\t"
+            "ds_read_b128 %3, %7\n\t"
+            "ds_read_b128 %4, %7 offset:16\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(h), "=&v"(qh0), "=&v"(qh1), "=&v"(q0), "=&v"(q1)
+            : "n"(VM), "v"(a), "v"(b)
+            : "memory");
+    }
+    // codes are 5-bit: nibble plus bit 2j (group 2j) or 2j+1 of high-plane
+    // byte c for column c (quant/decode.zig:162-166)
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t shift,
+                                         bool direct) const {
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hb[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
+        int ah = 0, al = 0, bh = 0, bl = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t lo = (w[k] & 0x0f0f0f0fu) | (((hb[k] >> (2 * j)) & 0x01010101u) << 4);
+            const uint32_t hi = ((w[k] >> 4) & 0x0f0f0f0fu) | (((hb[k] >> (2 * j + 1)) & 0x01010101u) << 4);
+            ah = dot4(lo, A.hi[k], ah);
+            al = dot4(lo, A.lo[k], al);
+            bh = dot4(hi, B.hi[k], bh);
+            bl = dot4(hi, B.lo[k], bl);
+        }
+        const float ia = (float)(ah * 256 + al), ib = (float)(bh * 256 + bl);
+        const float d = half_bits(h.x & 0xffffu), dmin = half_bits(h.x >> 16);
+        float sa, ma, sb, mb;
+        q4k_pair_f(h.y, h.z, h.w, shift, direct, sa, ma, sb, mb);
+        const float dt = fmaf(sa * A.scale, ia, (sb * B.scale) * ib);
+        const float off = fmaf(ma, A.sum, mb * B.sum);
+        return fmaf(d, dt, -(dmin * off));
+    }
+};
+
+template <>
+struct GdEnc<23> {  // IQ4_XS: 8-byte header + the pair's 32 code bytes (8-byte aligned)
+    static constexpr uint32_t BYTES = 136;
+    uint32_t h0, h1;
+    u32x4_t qa, qb;
+    template <int VM>
+    __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
+        const uint32_t a = lds_u8_addr(blk), b = a + 8 + 32 * j;
+        u32x4_t hh;
+        asm volatile(
+            "s_waitcnt vmcnt(%3)\n\t"
+            "ds_read_b64 %0, %4\n\t"
+            "ds_read2_b64 %1, %5 offset1:1\n\t"
+            "ds_read2_b64 %2, %5 offset0:2 offset1:3\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(hh.xy), "=&v"(qa), "=&v"(qb)
+            : "n"(VM), "v"(a), "v"(b)
+            : "memory");
+        h0 = hh.x;
+        h1 = hh.y;
+    }
+    // group 2j: code bytes 0-15 (qa), group 2j+1: bytes 16-31 (qb); byte k's
+    // low nibble is value k and its high nibble value 16+k of the group
+    // (quant/decode.zig:213-228); codes map to signed bytes by iq4_lookup.
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t, bool) const {
+        const uint32_t wa[4] = {qa.x, qa.y, qa.z, qa.w}, wb[4] = {qb.x, qb.y, qb.z, qb.w};
+        int ah = 0, al = 0, bh = 0, bl = 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t la = iq4_lookup(wa[m] & 0x0f0f0f0fu), ua = iq4_lookup((wa[m] >> 4) & 0x0f0f0f0fu);
+            const uint32_t lb = iq4_lookup(wb[m] & 0x0f0f0f0fu), ub = iq4_lookup((wb[m] >> 4) & 0x0f0f0f0fu);
+            ah = dot4(la, A.hi[m], ah);
+            al = dot4(la, A.lo[m], al);
+            ah = dot4(ua, A.hi[4 + m], ah);
+            al = dot4(ua, A.lo[4 + m], al);
+            bh = dot4(lb, B.hi[m], bh);
+            bl = dot4(lb, B.lo[m], bl);
+            bh = dot4(ub, B.hi[4 + m], bh);
+            bl = dot4(ub, B.lo[4 + m], bl);
+        }
+        const float ia = (float)(ah * 256 + al), ib = (float)(bh * 256 + bl);
+        const uint32_t sl = (h1 >> (8 * j)) & 0xffu, sh = h0 >> 16;
+        const int sa = (int)((sl & 15u) | (((sh >> (4 * j)) & 3u) << 4)) - 32;
+        const int sb = (int)((sl >> 4) | (((sh >> (4 * j + 2)) & 3u) << 4)) - 32;
+        const float d = half_bits(h0 & 0xffffu);
+        return d * fmaf((float)sa * A.scale, ia, ((float)sb * B.scale) * ib);
+    }
+};
 typedef __attribute__((address_space(1))) void gd_global_void_t;
 
 template <int CTRL>
@@ -426,8 +533,8 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <int SLOTS, int D>
-__global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+template <uint32_t ENC, int SLOTS, int D>
+__global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
                                                                       const float *__restrict__ x,
@@ -445,7 +552,9 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     const uint32_t set = wv / set_waves, kw = wv % set_waves;
     const uint32_t g = lane / (4 * SLOTS), slot = (lane >> 2) % SLOTS, j = lane & 3;
     constexpr uint32_t GROUPS = 64 / (4 * SLOTS);
-    constexpr uint32_t ROW_CHUNKS = SLOTS * 9;
+    constexpr uint32_t BYTES = GdEnc<ENC>::BYTES;
+    constexpr uint32_t ROW_CHUNKS = SLOTS * BYTES / 16;  // a row's SLOTS blocks (SLOTS even for IQ4_XS)
+    static_assert(GROUPS * ROW_CHUNKS == BYTES && BYTES <= GD_DMA_INSTRS * 64, "one step is BYTES chunks");
     const bool direct = j < 2;
     const uint32_t shift = direct ? 16 * j : 16 * j - 32;
     const uint32_t row_begin = blockIdx.x * rows_per_wg;
@@ -458,14 +567,15 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
 
     // This lane's chunk in each DMA instruction: row q within the step and
     // byte offset within the row (chunks past the step repeat the last one;
-    // blocks past the row read block 0, so every byte copied is real data).
+    // chunks past the row's last block read the row's first bytes, so every
+    // byte copied is real data).
     uint32_t dq[GD_DMA_INSTRS], doff[GD_DMA_INSTRS];
 #pragma unroll
     for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {
-        const uint32_t k = min(64 * n + lane, GD_STEP_CHUNKS - 1);
-        const uint32_t c = k % ROW_CHUNKS, blk = SLOTS * kw + c / 9;
+        const uint32_t k = min(64 * n + lane, BYTES - 1);
+        const uint32_t off = SLOTS * kw * BYTES + 16 * (k % ROW_CHUNKS);
         dq[n] = k / ROW_CHUNKS;
-        doff[n] = (blk < nblocks ? blk * 144 : 0) + 16 * (c % 9);
+        doff[n] = off + 16 <= nblocks * BYTES ? off : 0;
     }
 #define NUQ_GD_DMA(SLOT_, STEP_)                                                                              \
     _Pragma("unroll") for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {                                          \
@@ -508,7 +618,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
         xa.poison = xb.poison = 0.f;
     }
     const float poison = xa.poison + xb.poison;
-    const uint32_t role = (g * ROW_CHUNKS + slot * 9) * 16;
+    const uint32_t role = g * ROW_CHUNKS * 16 + slot * BYTES;
     const uint32_t spare = rows_per_wg * set_waves + wv;  // one spare partial per wave
 
     // Step i lives in ring slot i % D. As soon as a slot's bytes are in
@@ -518,10 +628,11 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     // waits for all of them.
 #define NUQ_GD_COMPUTE(SLOT_, STEP_, VM_, REFILL_)                                                                     \
     {                                                                                                       \
-        uint4 h, q0, q1;                                                                                    \
-        ring_read<VM_>(NUQ_GD_RING(SLOT_) + role, 16 + 32 * j, h, q0, q1);                                  \
+        GdEnc<ENC> e_;                                                                                      \
+        e_.template read<VM_>(NUQ_GD_RING(SLOT_) + role, j);                                                \
         REFILL_                                                                                             \
-        const float v = group_sum<4 * SLOTS>(poison + q4k_lane(h, q0, q1, xa, xb, shift, direct));          \
+        /* lanes past the row's last block read arbitrary copied bytes: select zero */                     \
+        const float v = group_sum<4 * SLOTS>(poison + (live ? e_.dot(xa, xb, j, shift, direct) : 0.f));      \
         const uint32_t row = first + (STEP_) * set_stride + g;                                              \
         /* every lane of the group holds the sum; rows past the range go to a spare slot */               \
         partial[row < row_end ? (row - row_begin) * set_waves + kw : spare] = v;                            \
@@ -554,8 +665,8 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_dma_kernel(const uint8
     }
 }
 
-template <int SLOTS, int D>
-static hipError_t launch_q4k_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
+template <uint32_t ENC, int SLOTS, int D>
+static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                                  const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu) {
     const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
     const uint32_t step_rows = 64 / (4 * SLOTS);
@@ -571,7 +682,7 @@ static hipError_t launch_q4k_dma(hipStream_t s, const uint8_t *w, uint64_t strid
                        ((size_t)rows_per_wg * set_waves + waves) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
-    hipLaunchKernelGGL((gemv_q4k_dma_kernel<SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(64 * waves),
+    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(64 * waves),
                        lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
     return hipGetLastError();
 }
@@ -609,11 +720,11 @@ hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride,
         const int dd = (c / 1000) % 10, st = (c / 10) % 10, pc = c % 10 ? c % 10 : 1;
         hipError_t e = hipErrorInvalidValue;
         if (cdiv(nblocks, 4) <= GI_MAX_SET_WAVES) {
-            if (dd == 2) e = launch_q4k_dma<4, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
-            else if (dd == 3) e = launch_q4k_dma<4, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
+            if (dd == 2) e = launch_dma<12, 4, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
+            else if (dd == 3) e = launch_dma<12, 4, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
         } else {
-            if (dd == 2) e = launch_q4k_dma<8, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
-            else if (dd == 3) e = launch_q4k_dma<8, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
+            if (dd == 2) e = launch_dma<12, 8, 2>(s, w, stride, rows, nblocks, x, y, st, pc);
+            else if (dd == 3) e = launch_dma<12, 8, 3>(s, w, stride, rows, nblocks, x, y, st, pc);
         }
         if (e != hipErrorInvalidValue || config > 0) return e;
         config = 0;  // the LDS does not fit: register kernel
@@ -635,6 +746,25 @@ hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride,
         NUQ_GI_CASE(2, 2, 8) NUQ_GI_CASE(2, 1, 8)
     }
 #undef NUQ_GI_CASE
+    return hipErrorInvalidValue;
+}
+
+// Q5_K / IQ4_XS decode GEMV on the DMA kernel (two ring slots). Returns
+// hipErrorInvalidValue when the shape does not fit (more than 128 blocks per
+// row, x and the rings beyond LDS, or IQ4_XS rows of an odd block count,
+// whose 136-byte blocks would end mid-chunk): the caller then uses the
+// generic kernel.
+hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                           uint32_t columns, const float *x, float *y) {
+    const uint32_t nblocks = columns / 256;
+    if (cdiv(nblocks, 8) > GI_MAX_SET_WAVES) return hipErrorInvalidValue;
+    const bool four = cdiv(nblocks, 4) <= GI_MAX_SET_WAVES;
+    if (encoding == 13)
+        return four ? launch_dma<13, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
+                    : launch_dma<13, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);
+    if (encoding == 23 && nblocks % 2 == 0)
+        return four ? launch_dma<23, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
+                    : launch_dma<23, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);
     return hipErrorInvalidValue;
 }
 

@@ -36,6 +36,8 @@ hipError_t launch_gemv(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const float *x, float *y, int rows_per_wave);
 hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                const float *x, float *y, int config);
+hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                           uint32_t columns, const float *x, float *y);
 hipError_t launch_generic(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                           uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                           uint64_t out_stride, uint32_t tokens);
