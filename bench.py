@@ -242,9 +242,15 @@ def main():
         extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
                                                              args.steps, args.warmup).items()
                                if k not in ("w", "x", "y0")}
+        for name, enc in (("q5k", nq.Q5_K), ("iq4xs", nq.IQ4_XS)):
+            extras[f"{name}_gate_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, enc, 17408, 5120,
+                                                                       args.steps, args.warmup).items()
+                                           if k not in ("w", "x", "y0")}
         if not only or "prefill" in only:
             extras["prefill_q6k_down_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q6_K, 5120, 17408, 4096)
             extras["prefill_q4k_gate_m512"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 512)
+            extras["prefill_q5k_gate_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q5_K, 17408, 5120, 4096)
+            extras["prefill_iq4xs_gate_m4096"] = bench_gemm(torch, nq, backend, stream, nq.IQ4_XS, 17408, 5120, 4096)
             for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
                 extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120,
                                                                    8, reps=200, warmup=20, kernel=kid)
@@ -272,7 +278,7 @@ def main():
                    "parity_normwise": normwise},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_q4k_dma_kernel<4, 2>",
+                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_dma_kernel<12, 4, 2>",
                      "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
         "cpu_baseline": cpu,
     }
