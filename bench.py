@@ -80,6 +80,7 @@ def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmu
     base = torch.from_numpy(w).cuda()
     mats = [nq.Matrix(encoding, rows, columns, base if i == 0 else base.clone()) for i in range(ncopies)]
     ys = [torch.empty(rows, device="cuda") for _ in range(ncopies)]
+    stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         for i in range(ncopies):
             backend.matvec(mats[i], x, ys[i])
@@ -127,6 +128,7 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
     m = nq.Matrix(encoding, rows, columns, wg)
     y = torch.empty((tokens, rows), device="cuda")
     k = nq.KERNEL_TILE if kernel is None else kernel
+    stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
@@ -148,6 +150,7 @@ def bench_layer(torch, nq, backend, stream, reps=20):
     weights = L.quantized_weights()
     dev = L.upload(weights)
     x = torch.from_numpy(gaussian(20, L.HIDDEN)).cuda()
+    stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         L.step(backend, dev, x)
         eager = dev.buffers["logits"].clone()

@@ -112,6 +112,11 @@ int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
 // The decode GEMV: Q4_K on the integer-dot K-split kernel, the other
 // encodings on the row-per-wave kernels.
 int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, float *out) {
+    if (m->encoding == NUQ_Q6_K) {
+        hipError_t e = nuq::launch_gemv_dma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                            (uint32_t)m->rows, (uint32_t)m->columns, x, out);
+        if (e != hipErrorInvalidValue) return hip_check(ctx, e, "q6_k gemv launch");
+    }
     if (m->encoding == NUQ_Q5_K || m->encoding == NUQ_IQ4_XS) {
         hipError_t e = nuq::launch_gemv_dma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
                                             (uint32_t)m->rows, (uint32_t)m->columns, x, out);

@@ -380,7 +380,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
 // instruction n moves chunk 64n + i), and the lanes then read their bytes
 // from LDS. Waves never read
 // another wave's ring, so only the wave's own vmcnt orders DMA and reads.
-constexpr uint32_t GD_DMA_INSTRS = 3, GD_SLOT_BYTES = GD_DMA_INSTRS * 64 * 16;
+// A ring slot holds INSTRS copy instructions of 64 lanes x 16 bytes.
 
 typedef __attribute__((address_space(3))) void gd_lds_void_t;
 typedef __attribute__((address_space(3))) uint8_t gd_lds_u8_t;
@@ -398,7 +398,7 @@ struct GdEnc;
 
 template <>
 struct GdEnc<12> {  // Q4_K: header + the pair's 32 code bytes
-    static constexpr uint32_t BYTES = 144;
+    static constexpr uint32_t BYTES = 144, INSTRS = (BYTES + 63) / 64;
     u32x4_t h, q0, q1;
     template <int VM>
     __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
@@ -422,7 +422,7 @@ struct GdEnc<12> {  // Q4_K: header + the pair's 32 code bytes
 
 template <>
 struct GdEnc<13> {  // Q5_K: header, the 32 high-plane bytes, the pair's 32 code bytes
-    static constexpr uint32_t BYTES = 176;
+    static constexpr uint32_t BYTES = 176, INSTRS = (BYTES + 63) / 64;
     u32x4_t h, qh0, qh1, q0, q1;
     template <int VM>
     __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
@@ -466,8 +466,111 @@ struct GdEnc<13> {  // Q5_K: header, the 32 high-plane bytes, the pair's 32 code
 };
 
 template <>
+struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 scales, d
+    static constexpr uint32_t BYTES = 210, INSTRS = (BYTES + 63) / 64;
+    u32x4_t l0, l1, l2, l3, h0, h1;
+    uint32_t sc, d16;
+    // Blocks sit at 2-byte offsets in the ring. Misaligned LDS reads return
+    // the right bytes but stall, so the fields are read as 4-byte aligned
+    // dword pairs one dword longer than needed and shifted into place with
+    // v_alignbyte_b32 (by 0 or 2 bytes, the block's offset mod 4).
+    template <int VM>
+    __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        const uint32_t a = lds_u8_addr(blk), sh = a & 3u;
+        const uint32_t ql = (a + 64 * (j >> 1)) & ~3u, qh = (a + 128 + 32 * (j >> 1)) & ~3u;
+        const uint32_t sca = (a + 192 + 4 * j) & ~3u, da = (a + 208) & ~3u;
+        u32x2_t q[9], hq[5], sp;
+        uint32_t dw;
+        asm volatile(
+            "s_waitcnt vmcnt(%16)\n\t"
+            "ds_read2_b32 %0, %17 offset1:1\n\t"
+            "ds_read2_b32 %1, %17 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %2, %17 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %3, %17 offset0:6 offset1:7\n\t"
+            "ds_read2_b32 %4, %17 offset0:8 offset1:9\n\t"
+            "ds_read2_b32 %5, %17 offset0:10 offset1:11\n\t"
+            "ds_read2_b32 %6, %17 offset0:12 offset1:13\n\t"
+            "ds_read2_b32 %7, %17 offset0:14 offset1:15\n\t"
+            "ds_read2_b32 %8, %17 offset0:16 offset1:17\n\t"
+            "ds_read2_b32 %9, %18 offset1:1\n\t"
+            "ds_read2_b32 %10, %18 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %11, %18 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %12, %18 offset0:6 offset1:7\n\t"
+            "ds_read2_b32 %13, %18 offset0:8 offset1:9\n\t"
+            "ds_read2_b32 %14, %19 offset1:1\n\t"
+            "ds_read_b32 %15, %20\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]),
+              "=&v"(q[7]), "=&v"(q[8]), "=&v"(hq[0]), "=&v"(hq[1]), "=&v"(hq[2]), "=&v"(hq[3]), "=&v"(hq[4]),
+              "=&v"(sp), "=&v"(dw)
+            : "n"(VM), "v"(ql), "v"(qh), "v"(sca), "v"(da)
+            : "memory");
+        uint32_t r[18], t[10];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            r[2 * k] = q[k].x;
+            r[2 * k + 1] = q[k].y;
+        }
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            t[2 * k] = hq[k].x;
+            t[2 * k + 1] = hq[k].y;
+        }
+        uint32_t o[16], p[8];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) o[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], sh);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) p[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+        l0 = u32x4_t{o[0], o[1], o[2], o[3]};
+        l1 = u32x4_t{o[4], o[5], o[6], o[7]};
+        l2 = u32x4_t{o[8], o[9], o[10], o[11]};
+        l3 = u32x4_t{o[12], o[13], o[14], o[15]};
+        h0 = u32x4_t{p[0], p[1], p[2], p[3]};
+        h1 = u32x4_t{p[4], p[5], p[6], p[7]};
+        sc = __builtin_amdgcn_alignbyte(sp.y, sp.x, sh);
+        d16 = (dw >> (8 * sh)) & 0xffffu;
+    }
+    // lane j: quarters q0 = 2(j&1) (x slice A) and q0+1 (slice B) of half
+    // j>>1; code of column c = nibble j&1 of ql[c] (ql[32 + c] for q0+1) |
+    // bits 2q of qh[c] as bits 4-5, minus 32 (quant/decode.zig:198-211);
+    // scale bytes: A columns 0-15, 16-31, then B's.
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t, bool) const {
+        const uint32_t la[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        const uint32_t lb[8] = {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w};
+        const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const uint32_t ls = 4 * (j & 1), hs = 4 * (j & 1);
+        int a0h = 0, a0l = 0, a1h = 0, a1l = 0, b0h = 0, b0l = 0, b1h = 0, b1l = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t ua = ((la[k] >> ls) & 0x0f0f0f0fu) | (((hb[k] >> hs) & 0x03030303u) << 4);
+            const uint32_t ub = ((lb[k] >> ls) & 0x0f0f0f0fu) | (((hb[k] >> (hs + 2)) & 0x03030303u) << 4);
+            // u - 32 per byte as a signed byte, without borrows between bytes
+            const uint32_t sa = ((ua | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            const uint32_t sb = ((ub | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            if (k < 4) {
+                a0h = dot4(sa, A.hi[k], a0h);
+                a0l = dot4(sa, A.lo[k], a0l);
+                b0h = dot4(sb, B.hi[k], b0h);
+                b0l = dot4(sb, B.lo[k], b0l);
+            } else {
+                a1h = dot4(sa, A.hi[k], a1h);
+                a1l = dot4(sa, A.lo[k], a1l);
+                b1h = dot4(sb, B.hi[k], b1h);
+                b1l = dot4(sb, B.lo[k], b1l);
+            }
+        }
+        const float s0 = (float)(int8_t)(sc & 0xffu), s1 = (float)(int8_t)((sc >> 8) & 0xffu);
+        const float s2 = (float)(int8_t)((sc >> 16) & 0xffu), s3 = (float)(int8_t)(sc >> 24);
+        const float ta = fmaf(s0, (float)(a0h * 256 + a0l), s1 * (float)(a1h * 256 + a1l));
+        const float tb = fmaf(s2, (float)(b0h * 256 + b0l), s3 * (float)(b1h * 256 + b1l));
+        return half_bits(d16) * fmaf(A.scale, ta, B.scale * tb);
+    }
+};
+
+template <>
 struct GdEnc<23> {  // IQ4_XS: 8-byte header + the pair's 32 code bytes (8-byte aligned)
-    static constexpr uint32_t BYTES = 136;
+    static constexpr uint32_t BYTES = 136, INSTRS = (BYTES + 63) / 64;
     uint32_t h0, h1;
     u32x4_t qa, qb;
     template <int VM>
@@ -538,8 +641,29 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
                                                                       const float *__restrict__ x,
-                                                                      float *__restrict__ y) {
+                                                                      float *__restrict__ y, uint32_t tail) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    if (tail && blockIdx.x == gridDim.x - 1) {
+        // The matrix's last row (rows is the count without it), when a row
+        // ends mid-chunk: its last copy would read past the weights, so this
+        // extra workgroup decodes it exactly against F32 x instead.
+        const uint8_t *rowp = w + (uint64_t)rows * stride;
+        float acc = 0.f;
+        for (uint32_t c = threadIdx.x; c < nblocks * 256; c += blockDim.x)
+            acc = fmaf(decode_value(ENC, rowp + (uint64_t)(c / 256) * GdEnc<ENC>::BYTES, c % 256), x[c], acc);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        float *sums = (float *)lds;
+        if ((threadIdx.x & 63) == 0) sums[threadIdx.x >> 6] = acc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.f;
+            for (uint32_t k = 0; k < (blockDim.x >> 6); ++k) t += sums[k];
+            y[rows] = t;
+        }
+        return;
+    }
+    constexpr uint32_t GD_DMA_INSTRS = GdEnc<ENC>::INSTRS, GD_SLOT_BYTES = GD_DMA_INSTRS * 64 * 16;
     const uint32_t nslices = nblocks * 8;
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
@@ -554,7 +678,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
     constexpr uint32_t GROUPS = 64 / (4 * SLOTS);
     constexpr uint32_t BYTES = GdEnc<ENC>::BYTES;
     constexpr uint32_t ROW_CHUNKS = SLOTS * BYTES / 16;  // a row's SLOTS blocks (SLOTS even for IQ4_XS)
-    static_assert(GROUPS * ROW_CHUNKS == BYTES && BYTES <= GD_DMA_INSTRS * 64, "one step is BYTES chunks");
+    static_assert(GROUPS * ROW_CHUNKS == BYTES && SLOTS * BYTES % 16 == 0, "one step is BYTES chunks");
     const bool direct = j < 2;
     const uint32_t shift = direct ? 16 * j : 16 * j - 32;
     const uint32_t row_begin = blockIdx.x * rows_per_wg;
@@ -567,15 +691,17 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
 
     // This lane's chunk in each DMA instruction: row q within the step and
     // byte offset within the row (chunks past the step repeat the last one;
-    // chunks past the row's last block read the row's first bytes, so every
-    // byte copied is real data).
+    // chunks that start past the row's last block read the row's first bytes,
+    // so every byte copied is real data). When a row is not a whole number of
+    // chunks its last chunk also copies the first bytes after it, which the
+    // host keeps inside the weights (see launch_gemv_dma).
     uint32_t dq[GD_DMA_INSTRS], doff[GD_DMA_INSTRS];
 #pragma unroll
     for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {
         const uint32_t k = min(64 * n + lane, BYTES - 1);
         const uint32_t off = SLOTS * kw * BYTES + 16 * (k % ROW_CHUNKS);
         dq[n] = k / ROW_CHUNKS;
-        doff[n] = off + 16 <= nblocks * BYTES ? off : 0;
+        doff[n] = off < nblocks * BYTES ? off : 0;
     }
 #define NUQ_GD_DMA(SLOT_, STEP_)                                                                              \
     _Pragma("unroll") for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {                                          \
@@ -667,23 +793,32 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
 
 template <uint32_t ENC, int SLOTS, int D>
 static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
-                                 const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu) {
+                                 const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu,
+                                 bool tail = false) {
+    // tail: the last row goes to one extra workgroup (see the kernel)
+    if (tail) {
+        if (rows < 2) return hipErrorInvalidValue;
+        rows -= 1;
+    }
+    const uint32_t cus = 256 * wgs_per_cu - (tail ? 1 : 0);
     const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
     const uint32_t step_rows = 64 / (4 * SLOTS);
     uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
     // Fewer wave sets for small matrices, so the grid still covers the CUs.
-    if (!sets_wanted) sets_wanted = std::max(1u, rows / (256 * wgs_per_cu * step_rows));
+    if (!sets_wanted) sets_wanted = std::max(1u, rows / (cus * step_rows));
     if (sets_wanted < sets) sets = sets_wanted;
-    const uint32_t unit = step_rows * sets;
-    const uint32_t per_wg = (rows + 256 * wgs_per_cu - 1) / (256 * wgs_per_cu);
-    const uint32_t rows_per_wg = (per_wg + unit - 1) / unit * unit;
+    // Rows per workgroup need not be whole set steps (each set guards its
+    // last step), so the grid is the CU count and each CU streams the same
+    // share of the bytes.
+    const uint32_t rows_per_wg = std::max(1u, (rows + cus - 1) / cus);
     const uint32_t waves = set_waves * sets;
-    const size_t lds = (size_t)waves * D * GD_SLOT_BYTES + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
+    const size_t lds = (size_t)waves * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
                        ((size_t)rows_per_wg * set_waves + waves) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
-    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(64 * waves),
-                       lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y);
+    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)),
+                       dim3(64 * waves), lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y,
+                       tail ? 1u : 0u);
     return hipGetLastError();
 }
 
@@ -749,7 +884,8 @@ hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride,
     return hipErrorInvalidValue;
 }
 
-// Q5_K / IQ4_XS decode GEMV on the DMA kernel (two ring slots). Returns
+// Q5_K / Q6_K / IQ4_XS decode GEMV on the DMA kernel (two ring slots; Q6_K
+// always with 8-block lane groups, so a row's segment is whole chunks). Returns
 // hipErrorInvalidValue when the shape does not fit (more than 128 blocks per
 // row, x and the rings beyond LDS, or IQ4_XS rows of an odd block count,
 // whose 136-byte blocks would end mid-chunk): the caller then uses the
@@ -762,6 +898,11 @@ hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, u
     if (encoding == 13)
         return four ? launch_dma<13, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
                     : launch_dma<13, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);
+    if (encoding == 14)
+        // A Q6_K row of nblocks % 8 != 0 blocks ends mid-chunk, so its last
+        // copy reads up to 8 bytes past it: the next row for all but the
+        // matrix's last row, which an extra workgroup computes directly.
+        return launch_dma<14, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1, nblocks * 210u % 16 != 0);
     if (encoding == 23 && nblocks % 2 == 0)
         return four ? launch_dma<23, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
                     : launch_dma<23, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);

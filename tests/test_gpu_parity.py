@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "decoder_fixtures.json").read_text())
 F32_K = 4e-6   # reference matvec bound (metal-check.zig:3976)
-INT_GEMV = {12, 13, 23}  # encodings whose M=1 GEMV runs on the integer-dot kernels
+INT_GEMV = {12, 13, 14, 23}  # encodings whose M=1 GEMV runs on the integer-dot kernels
 F16_K = 2e-3   # f16-rounded operands
 
 
@@ -130,6 +130,8 @@ GEMV_SHAPES = [
     (23, 35, 1280),       # odd block count: the generic kernel
     (13, 512, 17408),     # 8-block lane groups
     (23, 512, 17408),
+    (14, 64, 2048),       # Q6_K rows of whole 16-byte chunks
+    (14, 1, 256),         # one row: the row-per-wave kernel
 ]
 
 
