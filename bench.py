@@ -68,6 +68,43 @@ class Timer:
         self.ms = self.start.elapsed_time(self.end)
 
 
+def bench_upload(torch, nq, backend, total_bytes=1 << 30, reps=3):
+    """GGUF file -> device: a file of Q4_K 17408x5120 matrices (about 1 GiB)
+    written to a temporary directory (in the page cache), mapped and parsed
+    by libnuq, then its data section uploaded (nuq_gguf_upload). Reported
+    beside a plain torch copy of the same mapped bytes (pageable host
+    memory). Host-to-device over PCIe: never the headline value."""
+    import tempfile
+    from pathlib import Path
+
+    from nuclis_amd import gguf
+    from nuclis_amd.synth import write_gguf as write_model
+    w = nq.quantize(nq.Q4_K, np.full((1, 5120), 0.01, np.float32))
+    mat = np.tile(w.reshape(-1), 17408)
+    count = max(1, total_bytes // mat.nbytes)
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "upload.gguf"
+        write_model(path, [(f"blk.{i}.ffn_gate.weight", (5120, 17408), 12, mat) for i in range(count)])
+        with gguf.open(path) as doc:
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                dw = gguf.upload(backend, doc)
+                times.append(time.perf_counter() - t0)
+                del dw
+            mapped = np.memmap(path, dtype=np.uint8, mode="r")[doc.data_offset:]
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ref = torch.from_numpy(np.asarray(mapped)).cuda()
+            torch.cuda.synchronize()
+            plain = time.perf_counter() - t0
+            nbytes = doc.data_bytes
+            del ref, mapped
+    best = min(times)
+    return {"bytes": nbytes, "tensors": count, "seconds": [round(t, 4) for t in times],
+            "gbs_best": nbytes / best / 1e9, "torch_pageable_copy_gbs": nbytes / plain / 1e9}
+
+
 def copies_for(nbytes: int) -> int:
     return max(8, -(-2 * MALL_BYTES // nbytes))
 
@@ -242,6 +279,7 @@ def main():
         extras["q6k_lmhead_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q6_K, 151936, 5120,
                                                                    64, 8).items() if k not in ("w", "x", "y0")}
         extras["decode_layer_step"] = bench_layer(torch, nq, backend, stream)
+        extras["gguf_upload"] = bench_upload(torch, nq, backend)
         extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
                                                              args.steps, args.warmup).items()
                                if k not in ("w", "x", "y0")}

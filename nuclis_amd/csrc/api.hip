@@ -18,7 +18,13 @@
 #include <cstring>
 #include <string>
 
+#include <algorithm>
+#include <thread>
+#include <vector>
+
 #include "../../include/nuq.h"
+#include "../../include/nuq_gguf.h"
+#include "gguf_doc.h"
 #include "formats.h"
 #include "kernels.h"
 
@@ -401,4 +407,56 @@ int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *
     return NUQ_OK;
 }
 
+// The tensor-data section of a GGUF file goes to the device unchanged
+// (tensors keep their offsets). Host threads copy the mapping into one of
+// two pinned staging buffers while the DMA engine drains the other, so the
+// page-cache reads, the pinned copy and PCIe overlap.
+int nuq_gguf_upload(nuq_context *ctx, const nuq_gguf *g, void *device, uint64_t device_len) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (!g || (!device && device_len)) return fail(ctx, NUQ_INVALID_ARGUMENT, "null document or device pointer");
+    const uint64_t total = g->file_bytes - g->data_offset;
+    if (g->avail < g->file_bytes) return fail(ctx, NUQ_GGUF_END_OF_STREAM, "the tensor data is not all present");
+    if (device_len < total)
+        return fail(ctx, NUQ_INVALID_ARGUMENT, "device buffer of %llu bytes < data section of %llu",
+                    (unsigned long long)device_len, (unsigned long long)total);
+    if (total == 0) return NUQ_OK;
+    constexpr uint64_t CHUNK = 64ull << 20;
+    const uint64_t chunk = std::min(CHUNK, total);
+    uint8_t *stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    int rc = NUQ_OK;
+    for (int b = 0; b < 2 && rc == NUQ_OK; ++b) {
+        rc = hip_check(ctx, hipHostMalloc((void **)&stage[b], chunk, hipHostMallocDefault), "pinned staging");
+        if (rc == NUQ_OK) rc = hip_check(ctx, hipEventCreateWithFlags(&done[b], hipEventDisableTiming), "event");
+    }
+    const unsigned threads = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+    const uint8_t *src = g->bytes + g->data_offset;
+    for (uint64_t off = 0, k = 0; rc == NUQ_OK && off < total; off += chunk, ++k) {
+        const int b = (int)(k & 1);
+        const uint64_t n = std::min(chunk, total - off);
+        // the copy that last used this buffer must have drained it
+        if (k >= 2) {
+            rc = hip_check(ctx, hipEventSynchronize(done[b]), "staging wait");
+            if (rc != NUQ_OK) break;
+        }
+        const uint64_t part = (n + threads - 1) / threads;
+        std::vector<std::thread> pool;
+        for (unsigned t = 1; t < threads && t * part < n; ++t)
+            pool.emplace_back([&, t] { memcpy(stage[b] + t * part, src + off + t * part, std::min(part, n - t * part)); });
+        memcpy(stage[b], src + off, std::min(part, n));
+        for (auto &th : pool) th.join();
+        rc = hip_check(ctx, hipMemcpyAsync((uint8_t *)device + off, stage[b], n, hipMemcpyHostToDevice, ctx->stream),
+                       "upload copy");
+        if (rc == NUQ_OK) rc = hip_check(ctx, hipEventRecord(done[b], ctx->stream), "upload event");
+    }
+    const int sync = hip_check(ctx, hipStreamSynchronize(ctx->stream), "upload synchronize");
+    if (rc == NUQ_OK) rc = sync;
+    for (int b = 0; b < 2; ++b) {
+        if (done[b]) (void)hipEventDestroy(done[b]);
+        if (stage[b]) (void)hipHostFree(stage[b]);
+    }
+    return rc;
+}
+
 }  // extern "C"
+

@@ -1,8 +1,11 @@
-"""Seeded synthetic inputs shared by the tests, smoke() and bench.py.
+"""Seeded synthetic inputs shared by the tests, smoke() and bench.py, and a
+GGUF v3 writer for synthetic model files.
 
 Generator: numpy PCG64 (`np.random.default_rng(seed)`), standard normal
 draws in float32, scaled by the stated deviation. Weights are N(0, 0.02),
 activations N(0, 1), as the benchmark configurations specify."""
+import struct
+
 import numpy as np
 
 
@@ -11,3 +14,34 @@ def gaussian(seed: int, shape, std: float = 1.0) -> np.ndarray:
     if std != 1.0:
         out *= np.float32(std)
     return out
+
+
+def _gstr(text) -> bytes:
+    b = text.encode() if isinstance(text, str) else text
+    return struct.pack("<Q", len(b)) + b
+
+
+def write_gguf(path, tensors, metadata=None, alignment=32) -> None:
+    """GGUF v3 file: tensors = [(name, dims (GGUF order: columns first),
+    encoding, raw bytes)]; metadata = [(key, tag, packed value bytes)].
+    Tensor data is laid out in order, each at a multiple of `alignment`."""
+    meta = [(b"general.architecture", 8, _gstr("nuq-test")), (b"general.alignment", 4, struct.pack("<I", alignment))]
+    meta += [(k.encode() if isinstance(k, str) else k, t, v) for k, t, v in (metadata or [])]
+    out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)))
+    for k, t, v in meta:
+        out += _gstr(k) + struct.pack("<I", t) + v
+    offsets, at = [], 0
+    for _, _, _, raw in tensors:
+        offsets.append(at)
+        at += len(raw)
+        at += (alignment - at % alignment) % alignment
+    for (name, dims, enc, _), off in zip(tensors, offsets):
+        out += _gstr(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        out += struct.pack("<IQ", enc, off)
+    out += bytes((alignment - len(out) % alignment) % alignment)
+    data = bytearray(at)
+    for (_, _, _, raw), off in zip(tensors, offsets):
+        data[off:off + len(raw)] = np.asarray(raw, dtype=np.uint8).tobytes()
+    with open(path, "wb") as f:
+        f.write(out)
+        f.write(data)

@@ -1,4 +1,4 @@
-"""CPU-side checks of libnuq.so: it loads, exports every symbol include/nuq.h
+"""CPU-side checks of libnuq.so: it loads, exports every symbol include/*.h
 declares, validates rows as decode.validateRow does, and its host quantizers
 write blocks the oracle decodes (Q8_0 bit-identical to the reference encoder).
 No compute is launched: this file runs without a GPU."""
@@ -17,12 +17,12 @@ ROOT = Path(__file__).resolve().parents[1]
 
 
 def declared_functions():
-    text = (ROOT / "include" / "nuq.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(nuq_\w+)\(", text, re.M)))
 
 
 def test_header_and_python_binding_agree():
-    assert declared_functions() == sorted(nq.backend.EXPORTS)
+    assert declared_functions() == sorted(nq.backend.EXPORTS + nq.gguf.EXPORTS)
 
 
 def test_library_exports_every_declared_symbol():
