@@ -3,8 +3,8 @@
  *
  * Replaces the loading half of nuclis's weight path:
  *  - nuq_gguf_parse / nuq_gguf_open restate gguf.parse / gguf.parseDiagnosed
- *    (inference/src/formats/gguf.zig:301-398) and weights.Mapped.open
- *    (runtime/weights.zig:68-81): the header, metadata and tensor
+ *    (inference/src/formats/gguf.zig:311-410) and weights.Mapped.open
+ *    (runtime/weights.zig:63-78): the header, metadata and tensor
  *    descriptors are read and validated with the same limits, in the same
  *    order, to the same errors; no tensor weights are read.
  *  - nuq_gguf_upload copies the file's tensor-data section, unchanged, into
@@ -15,7 +15,7 @@
  *    alignment the vector kernels want for Q4_K / Q5_K rows.
  *
  * Status codes are the nuq_status values of nuq.h; the GGUF errors carry
- * the names of gguf.Error (gguf.zig:154-170) beside them.
+ * the names of gguf.Error (gguf.zig:156-172) beside them.
  */
 #ifndef NUQ_GGUF_H
 #define NUQ_GGUF_H
@@ -57,7 +57,7 @@ enum nuq_gguf_type {
     NUQ_GGUF_FLOAT64 = 12
 };
 
-/* gguf.Value's active field (gguf.zig:106-113). */
+/* gguf.Value's active field (gguf.zig:105-112). */
 enum nuq_gguf_value_kind {
     NUQ_GGUF_VALUE_UNSIGNED = 0, NUQ_GGUF_VALUE_SIGNED = 1, NUQ_GGUF_VALUE_FLOAT = 2,
     NUQ_GGUF_VALUE_BOOLEAN = 3, NUQ_GGUF_VALUE_STRING = 4, NUQ_GGUF_VALUE_ARRAY = 5
@@ -72,7 +72,7 @@ typedef struct nuq_gguf_limits {
     uint64_t array_items;
 } nuq_gguf_limits;
 
-/* gguf.Value plus gguf.Array (gguf.zig:48-57). Strings point into the
+/* gguf.Value plus gguf.Array (gguf.zig:49-57). Strings point into the
  * document and are not NUL-terminated. `retained` is the number of values an
  * array keeps (0 for a lazy array: read it with nuq_gguf_array_reader). */
 typedef struct nuq_gguf_value {
@@ -113,7 +113,7 @@ typedef struct nuq_gguf_info {
     uint64_t tensor_count;
 } nuq_gguf_info;
 
-/* gguf.Rejection (gguf.zig:259-283): the tensor behind an UnsupportedTensorType,
+/* gguf.Rejection (gguf.zig:287-301): the tensor behind an UnsupportedTensorType,
  * InvalidShape or Overflow rejection, its name truncated to 128 bytes.
  * has_encoding is 0 when the rank was refused before the encoding was read. */
 typedef struct nuq_gguf_rejection {
@@ -124,7 +124,7 @@ typedef struct nuq_gguf_rejection {
     uint32_t reserved;
 } nuq_gguf_rejection;
 
-/* gguf.ArrayReader (gguf.zig:62-104): bounded sequential access to a lazy
+/* gguf.ArrayReader (gguf.zig:63-104): bounded sequential access to a lazy
  * string or int32 array in a borrowed directory image. */
 typedef struct nuq_gguf_array_reader {
     const uint8_t *bytes;
@@ -139,13 +139,13 @@ typedef struct nuq_gguf nuq_gguf;
 
 void nuq_gguf_default_limits(nuq_gguf_limits *limits);
 
-/* gguf.parseDiagnosed (gguf.zig:301-398) over `avail` bytes of a file that
+/* gguf.parseDiagnosed (gguf.zig:311-410) over `avail` bytes of a file that
  * is `file_bytes` long (the bytes past `avail` are missing, as for a reader
  * that ends early). limits and rejection may be NULL (defaults / not asked).
  * The document borrows `bytes`, which must outlive it; *out is NULL on error. */
 int nuq_gguf_parse(const void *bytes, uint64_t avail, uint64_t file_bytes, const nuq_gguf_limits *limits,
                    nuq_gguf **out, nuq_gguf_rejection *rejection);
-/* weights.Mapped.open (runtime/weights.zig:68-81): maps `path` read-only and
+/* weights.Mapped.open (runtime/weights.zig:63-78): maps `path` read-only and
  * parses it; files of 0 bytes or above 128 GiB are LimitExceeded. */
 int nuq_gguf_open(const char *path, const nuq_gguf_limits *limits, nuq_gguf **out, nuq_gguf_rejection *rejection);
 /* Document.deinit / Mapped.deinit. */

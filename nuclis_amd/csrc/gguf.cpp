@@ -1,5 +1,5 @@
 // GGUF v3 directory reader (host only). Restates gguf.parseDiagnosed
-// (inference/src/formats/gguf.zig:301-398) over a byte span: same limits,
+// (inference/src/formats/gguf.zig:311-410) over a byte span: same limits,
 // same validation order, same errors. Tensor weights are never read here;
 // their byte ranges are validated. nuq_gguf_upload (api.hip) moves the data
 // section to the device.
@@ -23,7 +23,7 @@
 namespace {
 
 // gguf.retained_array_items / retained_key_prefixes / retained_prefixed_items
-// (gguf.zig:40-46).
+// (gguf.zig:41-47).
 constexpr uint64_t kRetainedArrayItems = 64;
 constexpr uint64_t kRetainedPrefixedItems = 65536;
 constexpr const char *kRetainedPrefixes[] = {"prism.hadamard."};
@@ -115,7 +115,7 @@ bool utf8_valid(const uint8_t *s, size_t n) {
     return true;
 }
 
-// validateName (gguf.zig:244-248)
+// validateName (gguf.zig:273-277)
 int validate_name(const std::string &name) {
     if (name.empty() || name.size() > 65535 || !utf8_valid((const uint8_t *)name.data(), name.size()))
         return NUQ_GGUF_INVALID_NAME;
@@ -136,7 +136,7 @@ bool retained_key(const std::string &key) {
         if (rc_ != NUQ_OK) return rc_; \
     } while (0)
 
-// gguf.zig:172-240 Cursor. `position` counts bytes consumed; advance checks
+// gguf.zig:174-266 Cursor. `position` counts bytes consumed; advance checks
 // the claimed file length, then the directory limit; a read past the bytes
 // actually present is EndOfStream, as for a reader that ends early.
 struct Cursor {
@@ -557,7 +557,7 @@ int nuq_gguf_directory(const nuq_gguf *g, const void **bytes, uint64_t *len) {
     return NUQ_OK;
 }
 
-// ArrayReader (gguf.zig:62-104)
+// ArrayReader (gguf.zig:63-104)
 int nuq_gguf_array_reader_init(nuq_gguf_array_reader *r, uint32_t element_type, uint64_t count, uint64_t file_offset,
                                const void *directory, uint64_t directory_len, const nuq_gguf_limits *limits) {
     if (!r || (!directory && directory_len)) return NUQ_INVALID_ARGUMENT;

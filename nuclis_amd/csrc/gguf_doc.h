@@ -9,7 +9,7 @@
 
 namespace nuq {
 
-// gguf.Value with gguf.Array's fields (inference/src/formats/gguf.zig:48-57, 106-113)
+// gguf.Value with gguf.Array's fields (inference/src/formats/gguf.zig:49-57, 105-112)
 struct GgufValue {
     uint32_t kind = 0, type = 0;
     uint64_t u = 0;

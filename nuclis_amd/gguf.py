@@ -2,11 +2,11 @@
 
 Mirrors nuclis's loader surface:
   - parse(bytes, file_bytes, limits, rejection) / open(path): gguf.parse,
-    gguf.parseDiagnosed (inference/src/formats/gguf.zig:301-398) and
-    weights.Mapped.open (runtime/weights.zig:68-81); errors are GgufError
+    gguf.parseDiagnosed (inference/src/formats/gguf.zig:311-410) and
+    weights.Mapped.open (runtime/weights.zig:63-78); errors are GgufError
     whose `.name` is the Zig error name.
-  - Document.get / Document.string (gguf.zig:141-152), Document.tensors.
-  - ArrayReader (gguf.zig:62-104) for lazy string / int32 arrays.
+  - Document.get / Document.string (gguf.zig:141-153), Document.tensors.
+  - ArrayReader (gguf.zig:63-104) for lazy string / int32 arrays.
   - Document.tensor_bytes / Document.host_matrix: weights.View.bytes and
     View.matrix (runtime/weights.zig:11-19) on the host mapping.
   - upload(backend, doc): the tensor-data section into one device buffer;
@@ -41,7 +41,7 @@ EXPORTS = [
 
 
 class GgufError(Exception):
-    """A gguf.Error (gguf.zig:154-170); `.name` is the Zig error name."""
+    """A gguf.Error (gguf.zig:156-172); `.name` is the Zig error name."""
 
     def __init__(self, code: int, message: str = ""):
         self.code = code
@@ -140,7 +140,7 @@ def _limits(limits: dict | None):
 
 @dataclass
 class Value:
-    """gguf.Value (gguf.zig:106-113) with gguf.Array's fields for arrays.
+    """gguf.Value (gguf.zig:105-112) with gguf.Array's fields for arrays.
     `value` is an int, float, bool or bytes; arrays carry `values` when the
     directory retained them (else None: read them with ArrayReader)."""
 
@@ -185,14 +185,14 @@ class Tensor:
 
 @dataclass
 class Rejection:
-    """gguf.Rejection (gguf.zig:259-283)."""
+    """gguf.Rejection (gguf.zig:287-301)."""
 
     tensor: bytes | None = None
     encoding_id: int | None = None
 
 
 class Document:
-    """A parsed directory (gguf.Document, gguf.zig:124-152). A document made
+    """A parsed directory (gguf.Document, gguf.zig:124-154). A document made
     by parse() borrows the bytes it was given and keeps a reference to them."""
 
     def __init__(self, handle: int, keep=None):
@@ -302,7 +302,7 @@ def parse(data, file_bytes: int | None = None, limits: dict | None = None,
 
 
 def open(path, limits: dict | None = None, rejection: Rejection | None = None) -> Document:  # noqa: A001
-    """weights.Mapped.open (runtime/weights.zig:68-81): maps the file and parses it."""
+    """weights.Mapped.open (runtime/weights.zig:63-78): maps the file and parses it."""
     h = ctypes.c_void_p()
     rej = _Rejection()
     code = _L().nuq_gguf_open(str(path).encode(), _limits(limits), ctypes.byref(h),
@@ -316,7 +316,7 @@ def open(path, limits: dict | None = None, rejection: Rejection | None = None) -
 
 
 class ArrayReader:
-    """gguf.ArrayReader (gguf.zig:62-104) over a borrowed directory image."""
+    """gguf.ArrayReader (gguf.zig:63-104) over a borrowed directory image."""
 
     def __init__(self, array: Value, directory: bytes, limits: dict | None = None):
         self._dir = bytes(directory)

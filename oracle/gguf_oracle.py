@@ -1,8 +1,8 @@
 """Pure-Python GGUF v3 directory reader. TEST INFRASTRUCTURE ONLY.
 
 A second, independent restatement of gguf.parseDiagnosed
-(inference/src/formats/gguf.zig:301-398) and gguf.ArrayReader
-(gguf.zig:62-104), used only by tests/ as the checker of libnuq's C++ reader.
+(inference/src/formats/gguf.zig:311-410) and gguf.ArrayReader
+(gguf.zig:63-104), used only by tests/ as the checker of libnuq's C++ reader.
 The product never imports it.
 
 `parse(data, file_bytes, limits)` returns a Document or raises GgufError whose
@@ -19,9 +19,9 @@ from dataclasses import dataclass, field
 # gguf.Limits (gguf.zig:13-19)
 DEFAULT_LIMITS = dict(directory_bytes=64 * 1024 * 1024, metadata_count=16_384, tensor_count=100_000,
                       string_bytes=1024 * 1024, array_items=4_000_000)
-RETAINED_ARRAY_ITEMS = 64  # gguf.zig:40
-RETAINED_KEY_PREFIXES = ("prism.hadamard.",)  # gguf.zig:45
-RETAINED_PREFIXED_ITEMS = 65_536  # gguf.zig:46
+RETAINED_ARRAY_ITEMS = 64  # gguf.zig:41
+RETAINED_KEY_PREFIXES = ("prism.hadamard.",)  # gguf.zig:46
+RETAINED_PREFIXED_ITEMS = 65_536  # gguf.zig:47
 
 # gguf.Type (gguf.zig:21-35)
 UINT8, INT8, UINT16, INT16, UINT32, INT32, FLOAT32, BOOLEAN, STRING, ARRAY, UINT64, INT64, FLOAT64 = range(13)
@@ -109,7 +109,7 @@ def byte_count(layout, dims) -> int:
 
 
 def _validate_name(name: bytes) -> None:
-    """validateName (gguf.zig:244-248)."""
+    """validateName (gguf.zig:273-277)."""
     if len(name) == 0 or len(name) > 65_535:
         raise GgufError("InvalidName")
     try:
@@ -121,7 +121,7 @@ def _validate_name(name: bytes) -> None:
 
 
 class _Cursor:
-    """gguf.zig:172-240."""
+    """gguf.zig:174-266."""
 
     def __init__(self, data: bytes, file_bytes: int, limits: dict):
         self.data, self.file_bytes, self.limits, self.position = data, file_bytes, limits, 0
@@ -199,7 +199,7 @@ class _Cursor:
 
 def parse(data: bytes, file_bytes: int | None = None, limits: dict | None = None,
           rejection: Rejection | None = None) -> Document:
-    """gguf.parseDiagnosed (gguf.zig:301-398)."""
+    """gguf.parseDiagnosed (gguf.zig:311-410)."""
     lim = dict(DEFAULT_LIMITS, **(limits or {}))
     if file_bytes is None:
         file_bytes = len(data)
@@ -276,7 +276,7 @@ def parse(data: bytes, file_bytes: int | None = None, limits: dict | None = None
 
 
 def read_array(element_type: int, count: int, file_offset: int, directory: bytes, limits: dict | None = None):
-    """ArrayReader.init then next* until the end (gguf.zig:62-104): a list of
+    """ArrayReader.init then next* until the end (gguf.zig:63-104): a list of
     values, or GgufError at the failing step (after the values read so far)."""
     lim = dict(DEFAULT_LIMITS, **(limits or {}))
     if len(directory) > lim["directory_bytes"] or count > lim["array_items"]:

@@ -1,7 +1,7 @@
 """GGUF wire-format builders for the tests.
 
 `fixture(**options)` writes the same bytes as the reference's test fixture
-(inference/src/formats/gguf.zig:424-470, FixtureOptions and fixture()): the
+(inference/src/formats/gguf.zig:424-471, FixtureOptions and fixture()): the
 header, three metadata entries (architecture, alignment, a two-string token
 array), two rank-1 tensors and 64 bytes of zero data. `write_model` (in
 nuclis_amd.synth) writes real GGUF v3 files for the device-upload tests.
@@ -35,7 +35,7 @@ def fixture(version=3, alignment=32, duplicate_metadata=False, duplicate_tensor=
 
 
 # Byte offset of the first metadata entry's type tag: the 24-byte fixed
-# header, the key's length, then the key (gguf.zig:688).
+# header, the key's length, then the key (gguf.zig:666).
 FIRST_TAG = 24 + 8 + len("general.architecture")
 
 

@@ -1,6 +1,6 @@
 """GGUF directory reader: libnuq's C++ parser (nuclis_amd.gguf) against the
 reference's own tests (inference/src/formats/gguf.zig:424-772,
-runtime/weights.zig:84-103) and against the independent Python restatement
+runtime/weights.zig:87-103) and against the independent Python restatement
 in oracle/gguf_oracle.py, case by case and over the reference's corruption
 families. Host only: no GPU work."""
 import random
@@ -50,7 +50,7 @@ def both(data, file_bytes=None, limits=None):
     return a
 
 
-# -- gguf.zig:493-504 ------------------------------------------------------------
+# -- gguf.zig:512-523 ------------------------------------------------------------
 def test_read_metadata_and_tensor_ranges_without_consuming_weights():
     data = fixture()
     kind, s = both(data)
@@ -66,7 +66,7 @@ def test_read_metadata_and_tensor_ranges_without_consuming_weights():
         assert doc.data_offset % 32 == 0 and len(data) - doc.data_offset == 64
 
 
-# -- gguf.zig:473-491 ------------------------------------------------------------
+# -- gguf.zig:473-502 ------------------------------------------------------------
 def test_a_rejected_tensor_is_named_for_the_caller_that_asks():
     for opts, err, enc in (({"encoding_id": 999}, "UnsupportedTensorType", 999),
                            ({"encoding_id": 12, "dimension": 100}, "InvalidShape", 12),
@@ -95,7 +95,7 @@ def test_rank_rejection_names_the_tensor_without_an_encoding():
         assert e.value.name == "InvalidShape" and rej.tensor == b"first" and rej.encoding_id is None
 
 
-# -- gguf.zig:525-554 ------------------------------------------------------------
+# -- gguf.zig:525-547 ------------------------------------------------------------
 def test_lazy_array_access_bounds_offsets_counts_strings_and_element_types():
     b = b"\x01\x00\x00\x00\x00\x00\x00\x00a"
     desc = gguf.Value("array", 9, None, gguf.STRING, 1, 0)
@@ -149,7 +149,7 @@ def test_lazy_token_array_reads_back_through_the_directory():
     assert og.read_array(og.STRING, 2, tokens.file_offset, data) == got
 
 
-# -- gguf.zig:556-572 ------------------------------------------------------------
+# -- gguf.zig:549-566 ------------------------------------------------------------
 def test_truncated_directory_and_tensor_payloads_fail_cleanly():
     data = fixture()
     with gguf.parse(data) as doc:
@@ -159,7 +159,7 @@ def test_truncated_directory_and_tensor_payloads_fail_cleanly():
         assert kind == "error" and name in ("EndOfStream", "TensorOutOfBounds"), (n, name)
 
 
-# -- gguf.zig:574-595 ------------------------------------------------------------
+# -- gguf.zig:568-590 ------------------------------------------------------------
 @pytest.mark.parametrize("opts,expected", [
     ({"version": 2}, "UnsupportedVersion"),
     ({"alignment": 0}, "InvalidAlignment"),
@@ -178,7 +178,7 @@ def test_reject_unsupported_containers_duplicates_invalid_layouts_and_ranges(opt
     assert both(fixture(**opts)) == ("error", expected)
 
 
-# -- gguf.zig:597-613 ------------------------------------------------------------
+# -- gguf.zig:592-615 ------------------------------------------------------------
 def test_hostile_lengths_and_counts_are_rejected_before_allocating():
     data = fixture()
     for lim in ({"tensor_count": 1}, {"metadata_count": 1}, {"directory_bytes": 24}, {"string_bytes": 4},
@@ -189,7 +189,7 @@ def test_hostile_lengths_and_counts_are_rejected_before_allocating():
     assert both(bytes(hostile)) == ("error", "LimitExceeded")
 
 
-# -- gguf.zig:663-676, 678-691 -------------------------------------------------------
+# -- gguf.zig:658-670, 672-684 -------------------------------------------------------
 def test_reject_bad_magic_and_unknown_metadata_tags():
     data = bytearray(fixture())
     data[0] = ord("X")
@@ -208,7 +208,7 @@ def test_invalid_boolean_values_and_nested_arrays_are_explicit_errors():
     assert both(bytes(data)) == ("error", "UnsupportedNestedArray")
 
 
-# -- gguf.zig:693-717 ------------------------------------------------------------
+# -- gguf.zig:686-709 ------------------------------------------------------------
 def test_retain_small_numeric_arrays_while_leaving_large_arrays_as_descriptors():
     body = header(0, 2) + array_i32("sections", [i - 1 for i in range(4)]) + array_i32("large", [i - 1 for i in range(65)])
     data = pad32(body)
@@ -221,7 +221,7 @@ def test_retain_small_numeric_arrays_while_leaving_large_arrays_as_descriptors()
         assert [r.next_int32() for _ in range(65)] == [i - 1 for i in range(65)] and r.next_int32() is None
 
 
-# -- gguf.zig:719-751 ------------------------------------------------------------
+# -- gguf.zig:711-745 ------------------------------------------------------------
 def test_arrays_under_a_retained_key_prefix_keep_every_value_strings_included():
     body = header(0, 3) + array_i32("prism.hadamard.sign_values", [1 if i % 2 == 0 else -1 for i in range(65)])
     body += array_str("prism.hadamard.weight_names", ["output.weight", "blk.0.ffn_up.weight"])
@@ -241,7 +241,7 @@ def test_retained_prefix_arrays_have_their_own_limit():
     assert both(pad32(body)) == ("error", "LimitExceeded")
 
 
-# -- gguf.zig:763-772: the fuzz seed ------------------------------------------------
+# -- gguf.zig:756-772: the fuzz seed ------------------------------------------------
 def test_fuzz_seed_parses():
     seed = header(1, 1) + gstr("general.alignment") + struct.pack("<II", 4, 32)
     seed += gstr("w") + struct.pack("<IQIQ", 1, 4, 0, 0) + bytes(6) + bytes([0x3F]) * 16
@@ -251,7 +251,7 @@ def test_fuzz_seed_parses():
         assert both(short)[0] == "error"
 
 
-# -- gguf.zig:624-661: corruption families, product vs oracle -------------------------
+# -- gguf.zig:617-650: corruption families, product vs oracle -------------------------
 def test_corrupted_files_agree_with_the_oracle():
     good = fixture()
     n = len(good)
@@ -282,7 +282,7 @@ def test_corrupted_files_agree_with_the_oracle():
 
 
 def test_truncation_and_directory_limit_are_judged_in_the_reference_order():
-    # Cursor.advance (gguf.zig:179-187) checks the file's end before the
+    # Cursor.advance (gguf.zig:180-188) checks the file's end before the
     # directory limit: a read past both is EndOfStream.
     good = fixture()
     for k in range(0, 120, 3):
