@@ -105,6 +105,45 @@ def bench_upload(torch, nq, backend, total_bytes=1 << 30, reps=3):
             "gbs_best": nbytes / best / 1e9, "torch_pageable_copy_gbs": nbytes / plain / 1e9}
 
 
+def bench_sampling(torch, nq, backend, stream, vocab=151936, reps=200):
+    """Device sampling at the config-3 vocabulary: the partial top-k (k=256,
+    sort passes + exp-sum) and the history penalties, each graph-captured and
+    replayed `reps` times; microseconds per call."""
+    import ctypes
+    from nuclis_amd.synth import gaussian
+    L = nq.lib()
+    logits = torch.from_numpy(gaussian(70, vocab) * 3).cuda()
+    values = torch.empty(256, device="cuda")
+    indices = torch.empty(256, dtype=torch.int32, device="cuda")
+    sums = torch.empty(64, device="cuda")
+    flags = torch.empty(64, dtype=torch.int32, device="cuda")
+    words = torch.zeros((vocab + 31) // 32, dtype=torch.int32, device="cuda")
+    words[::7] = 0x01010101
+    bufs = nq.backend._TopKBuffers(values.data_ptr(), indices.data_ptr(), sums.data_ptr(), flags.data_ptr())
+    out = {}
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        L.nuq_set_stream(backend._h, stream.cuda_stream)
+        calls = {
+            "topk256": lambda: L.nuq_topk(backend._h, logits.data_ptr(), vocab, 256, 0.7, ctypes.byref(bufs)),
+            "penalize": lambda: L.nuq_penalize(backend._h, logits.data_ptr(), vocab, words.data_ptr(), words.numel(),
+                                               1.0, 0.0),
+        }
+        for name, fn in calls.items():
+            assert fn() == 0
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(reps):
+                    assert fn() == 0
+            graph.replay()
+            torch.cuda.synchronize()
+            with Timer(torch, stream) as t:
+                graph.replay()
+            out[f"{name}_us"] = t.ms * 1e3 / reps
+    out["vocab"] = vocab
+    return out
+
+
 def copies_for(nbytes: int) -> int:
     return max(8, -(-2 * MALL_BYTES // nbytes))
 
@@ -280,6 +319,7 @@ def main():
                                                                    64, 8).items() if k not in ("w", "x", "y0")}
         extras["decode_layer_step"] = bench_layer(torch, nq, backend, stream)
         extras["gguf_upload"] = bench_upload(torch, nq, backend)
+        extras["sampling"] = bench_sampling(torch, nq, backend, stream)
         extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
                                                              args.steps, args.warmup).items()
                                if k not in ("w", "x", "y0")}

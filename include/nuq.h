@@ -103,7 +103,7 @@ int nuq_validate_row(uint32_t encoding, uint64_t byte_count, uint64_t element_co
  * bit-exact with the CPU decoder (quant/decode.zig:30). */
 int nuq_embed(nuq_context *ctx, const nuq_matrix *m, uint32_t token, float *out);
 /* Bulk form of embed: rows [first, first+count) to out[count][columns]. */
-int nuq_dequant_rows(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uint64_t count, float *out);
+int nuq_dequant_range(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uint64_t count, float *out);
 
 /* Backend.matvec (ops/matvec.zig:32-34, 85-116): out[r] = sum_c W[r,c] x[c],
  * x and out F32. The decode GEMV. */
@@ -136,6 +136,45 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
  * maximum wins; a non-finite logit gives NUQ_NON_FINITE). `index` is a host
  * pointer; the call synchronizes the context's stream. */
 int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *index);
+
+/* Flat-argument forms of dequant / matvec / matmul over `rows` rows of
+ * `stride` bytes at `w` (stride = the encoded row length, as cpu.Matrix
+ * requires): the same validation, routing and kernels as nuq_dequant_range
+ * (all rows), nuq_matvec and nuq_matmul. For callers that hold raw pointers
+ * rather than a matrix descriptor (C / C++ harnesses). */
+int nuq_dequant_rows(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows,
+                     uint32_t columns, float *out);
+int nuq_gemv(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows, uint32_t columns,
+             const float *x, float *y);
+int nuq_gemm(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows, uint32_t columns,
+             const void *x, uint32_t x_dtype, uint64_t in_stride, float *y, uint64_t out_stride, uint32_t tokens);
+
+/* Device sampling: the partial top-k readback (Backend.topk,
+ * backends/metal/ops/sampling.zig:15-57). `values` / `indices` receive the k
+ * best logits by (value descending, index ascending); `sums` the
+ * NUQ_TOPK_PARTIALS F32 partial sums of exp((l - max) / temperature) over
+ * every logit, which the caller adds in F64 (sampling.TopK.total); `flags`
+ * one word per partition, nonzero when it saw a non-finite logit. NaN never
+ * enters the list. All four are device buffers (k floats, k u32,
+ * NUQ_TOPK_PARTIALS floats, NUQ_TOPK_PARTIALS u32). */
+enum { NUQ_TOPK_CAPACITY = 256, NUQ_TOPK_PARTIALS = 64, NUQ_TOPK_MAX_COUNT = 262144 };
+typedef struct nuq_topk_buffers {
+    float *values;
+    uint32_t *indices;
+    float *sums;
+    uint32_t *flags;
+} nuq_topk_buffers;
+/* Backend.topk: InvalidShape unless 0 < count <= NUQ_TOPK_MAX_COUNT,
+ * 0 < k <= min(NUQ_TOPK_CAPACITY, count) and the temperature is finite and
+ * positive. Enqueued on the context's stream (no synchronization). */
+int nuq_topk(nuq_context *ctx, const float *logits, uint64_t count, uint32_t k, float temperature,
+             const nuq_topk_buffers *out);
+/* Backend.penalize (ops/sampling.zig:58-71) = Sampler.penalize
+ * (sampling/root.zig:375-381) in place on every logit whose id is set in
+ * `history` (bit id of word id / 32; history_words >= ceil(count / 32)):
+ * l / repetition for l > 0, else l * repetition, then minus presence. */
+int nuq_penalize(nuq_context *ctx, float *logits, uint64_t count, const uint32_t *history, uint64_t history_words,
+                 float repetition, float presence);
 
 /* Weight preparation on the host (not part of the reference's backend):
  * quantize `rows` F32 rows of `columns` into GGUF rows in dst (host memory,

@@ -75,6 +75,29 @@ class _Matrix(ctypes.Structure):
                 ("columns", ctypes.c_uint64), ("bytes", ctypes.c_void_p), ("byte_len", ctypes.c_uint64)]
 
 
+class _TopKBuffers(ctypes.Structure):
+    _fields_ = [("values", ctypes.c_void_p), ("indices", ctypes.c_void_p), ("sums", ctypes.c_void_p),
+                ("flags", ctypes.c_void_p)]
+
+
+# Backend.topk limits (backends/metal/ops/sampling.zig:15-22)
+TOPK_CAPACITY, TOPK_PARTIALS, TOPK_MAX_COUNT = 256, 64, 262144
+
+
+@dataclass
+class TopK:
+    """sampling.TopK (sampling/root.zig:154-173): the `count` best logits by
+    (value descending, id ascending), Σ exp((l − max) / temperature) over every
+    logit as the F64 sum of the device's F32 partial sums, and whether every
+    logit was finite."""
+
+    temperature: float
+    ids: list
+    values: list
+    total: float
+    finite: bool
+
+
 class _Segment(ctypes.Structure):
     _fields_ = [("matrix", _Matrix), ("output", ctypes.c_void_p)]
 
@@ -83,8 +106,9 @@ _lib = None
 
 EXPORTS = [
     "nuq_create", "nuq_destroy", "nuq_set_stream", "nuq_sync", "nuq_last_error", "nuq_set_generic_only",
-    "nuq_validate_row", "nuq_embed", "nuq_dequant_rows", "nuq_matvec", "nuq_matvec_rows", "nuq_matmul",
-    "nuq_matmul_kernel", "nuq_matvec_segments", "nuq_argmax", "nuq_quantize_rows",
+    "nuq_validate_row", "nuq_embed", "nuq_dequant_range", "nuq_matvec", "nuq_matvec_rows", "nuq_matmul",
+    "nuq_matmul_kernel", "nuq_matvec_segments", "nuq_argmax", "nuq_quantize_rows", "nuq_dequant_rows", "nuq_gemv",
+    "nuq_gemm", "nuq_topk", "nuq_penalize",
 ]
 
 
@@ -108,7 +132,12 @@ def lib() -> ctypes.CDLL:
         L.nuq_set_generic_only.argtypes = [vp, ctypes.c_int]
         L.nuq_validate_row.argtypes = [u32, u64, u64]
         L.nuq_embed.argtypes = [vp, mp, u32, vp]
-        L.nuq_dequant_rows.argtypes = [vp, mp, u64, u64, vp]
+        L.nuq_dequant_range.argtypes = [vp, mp, u64, u64, vp]
+        L.nuq_dequant_rows.argtypes = [vp, u32, vp, u64, u32, u32, vp]
+        L.nuq_gemv.argtypes = [vp, u32, vp, u64, u32, u32, vp, vp]
+        L.nuq_gemm.argtypes = [vp, u32, vp, u64, u32, u32, vp, u32, u64, vp, u64, u32]
+        L.nuq_topk.argtypes = [vp, vp, u64, u32, ctypes.c_float, ctypes.POINTER(_TopKBuffers)]
+        L.nuq_penalize.argtypes = [vp, vp, u64, vp, u64, ctypes.c_float, ctypes.c_float]
         L.nuq_matvec.argtypes = [vp, mp, vp, vp]
         L.nuq_matvec_rows.argtypes = [vp, mp, vp, u64, vp, u64, u32]
         L.nuq_matmul.argtypes = [vp, mp, vp, u32, u64, vp, u64, u32]
@@ -224,7 +253,7 @@ class Backend:
 
     def dequant_rows(self, matrix: Matrix, first: int, count: int, output) -> None:
         m = matrix.c()
-        self._call(lib().nuq_dequant_rows, ctypes.byref(m), first, count, _ptr(output))
+        self._call(lib().nuq_dequant_range, ctypes.byref(m), first, count, _ptr(output))
 
     def matvec(self, matrix: Matrix, input, output) -> None:
         m = matrix.c()
@@ -252,6 +281,32 @@ class Backend:
             arr[i].matrix = mat.c()
             arr[i].output = _ptr(out)
         self._call(lib().nuq_matvec_segments, arr, len(segments), _ptr(input), mode)
+
+    def penalize(self, logits, history_words, repetition: float, presence: float, count: int | None = None) -> None:
+        """Backend.penalize (backends/metal/ops/sampling.zig:58-71), in place.
+        `history_words` is a device uint32/int32 tensor: bit id of word id / 32."""
+        n = logits.numel() if count is None else count
+        self._call(lib().nuq_penalize, _ptr(logits), n, _ptr(history_words), history_words.numel(), repetition,
+                   presence)
+
+    def topk(self, logits, k: int, temperature: float, count: int | None = None) -> TopK:
+        """Backend.topk (backends/metal/ops/sampling.zig:44-57) and the host's
+        readback into sampling.TopK; synchronizes the stream."""
+        torch = self._torch
+        dev = logits.device
+        values = torch.empty(max(k, 1), dtype=torch.float32, device=dev)
+        indices = torch.empty(max(k, 1), dtype=torch.int32, device=dev)
+        sums = torch.empty(TOPK_PARTIALS, dtype=torch.float32, device=dev)
+        flags = torch.empty(TOPK_PARTIALS, dtype=torch.int32, device=dev)
+        bufs = _TopKBuffers(values.data_ptr(), indices.data_ptr(), sums.data_ptr(), flags.data_ptr())
+        n = logits.numel() if count is None else count
+        self._call(lib().nuq_topk, _ptr(logits), n, k, temperature, ctypes.byref(bufs))
+        self.sync()
+        total = 0.0
+        for partial in sums.cpu().tolist():  # F64, in partition order
+            total += partial
+        return TopK(temperature, [int(i) & 0xffffffff for i in indices.cpu().tolist()[:k]],
+                    values.cpu().tolist()[:k], total, not bool(flags.cpu().any()))
 
     def argmax(self, logits) -> int:
         idx = ctypes.c_uint32(0)

@@ -16,7 +16,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnuq.so"
-SOURCES = ["api.hip", "gemv.hip", "gemv_int.hip", "gemm.hip", "quantize.cpp", "gguf.cpp"]
+SOURCES = ["api.hip", "gemv.hip", "gemv_int.hip", "gemm.hip", "sampling.hip", "quantize.cpp", "gguf.cpp"]
 ARCH = "gfx950"
 
 

@@ -12,6 +12,7 @@
 // (ops/matvec.zig:196-219, ops/matmul.zig:114-123): the vectorised kernels
 // need 16-byte aligned Q4_K rows (pointer and stride), even Q6_K / Q8_0 rows
 // and a 16-byte aligned input; anything else runs the generic control.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -35,6 +36,7 @@ struct nuq_context {
     std::string last_error;
     uint32_t *argmax_buf = nullptr;  // device: {index, nonfinite flag}
     nuq::SplitScratch split{nullptr, 0};  // prefill K-split workspace
+    uint64_t *topk_keys = nullptr;        // partial top-k keys between passes
 };
 
 namespace {
@@ -239,6 +241,11 @@ nuq_context *nuq_create(int device, char *err, size_t cap) {
         return nullptr;
     }
     ctx->split.tiles = tiles;
+    if (hipMalloc((void **)&ctx->topk_keys, nuq::topk_scratch_keys() * sizeof(uint64_t)) != hipSuccess) {
+        report("hipMalloc of the top-k scratch failed");
+        nuq_destroy(ctx);
+        return nullptr;
+    }
     return ctx;
 }
 
@@ -247,6 +254,7 @@ void nuq_destroy(nuq_context *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->argmax_buf) (void)hipFree(ctx->argmax_buf);
     if (ctx->split.work) (void)hipFree(ctx->split.work);
+    if (ctx->topk_keys) (void)hipFree(ctx->topk_keys);
     delete ctx;
 }
 
@@ -274,7 +282,7 @@ int nuq_validate_row(uint32_t encoding, uint64_t byte_count, uint64_t element_co
     return validate_row(encoding, byte_count, element_count);
 }
 
-int nuq_dequant_rows(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uint64_t count, float *out) {
+int nuq_dequant_range(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uint64_t count, float *out) {
     if (!ctx) return NUQ_INVALID_ARGUMENT;
     uint64_t stride;
     int e = check_matrix(ctx, m, &stride);
@@ -294,7 +302,7 @@ int nuq_embed(nuq_context *ctx, const nuq_matrix *m, uint32_t token, float *out)
     if (!ctx) return NUQ_INVALID_ARGUMENT;
     if (m && token >= m->rows) return fail(ctx, NUQ_INVALID_SHAPE, "token %u outside %llu rows", token,
                                            (unsigned long long)m->rows);
-    return nuq_dequant_rows(ctx, m, token, 1, out);
+    return nuq_dequant_range(ctx, m, token, 1, out);
 }
 
 int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out) {
@@ -339,6 +347,44 @@ int nuq_matmul(nuq_context *ctx, const nuq_matrix *m, const void *x, uint32_t x_
 int nuq_matmul_kernel(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const void *x, uint32_t x_dtype,
                       uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
     return matmul_impl(ctx, kernel, m, x, x_dtype, in_stride, out, out_stride, tokens);
+}
+
+// Flat-argument forms: a matrix of `rows` rows of `stride` bytes each, as
+// the descriptor entry points validate it (stride must be the encoded row
+// length, cpu/root.zig:31-36).
+static nuq_matrix flat_matrix(uint32_t encoding, const void *w, uint64_t stride, uint32_t rows, uint32_t columns) {
+    nuq_matrix m;
+    m.encoding = encoding;
+    m.reserved = 0;
+    m.rows = rows;
+    m.columns = columns;
+    m.bytes = w;
+    m.byte_len = stride * rows;
+    return m;
+}
+
+int nuq_dequant_rows(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows,
+                     uint32_t columns, float *out) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (rows != 0 && stride > UINT64_MAX / rows) return fail(ctx, NUQ_INVALID_BYTE_LENGTH, "rows x stride overflows");
+    const nuq_matrix m = flat_matrix(encoding, w, stride, rows, columns);
+    return nuq_dequant_range(ctx, &m, 0, rows, out);
+}
+
+int nuq_gemv(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows, uint32_t columns,
+             const float *x, float *y) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (rows != 0 && stride > UINT64_MAX / rows) return fail(ctx, NUQ_INVALID_BYTE_LENGTH, "rows x stride overflows");
+    const nuq_matrix m = flat_matrix(encoding, w, stride, rows, columns);
+    return nuq_matvec(ctx, &m, x, y);
+}
+
+int nuq_gemm(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride, uint32_t rows, uint32_t columns,
+             const void *x, uint32_t x_dtype, uint64_t in_stride, float *y, uint64_t out_stride, uint32_t tokens) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (rows != 0 && stride > UINT64_MAX / rows) return fail(ctx, NUQ_INVALID_BYTE_LENGTH, "rows x stride overflows");
+    const nuq_matrix m = flat_matrix(encoding, w, stride, rows, columns);
+    return nuq_matmul(ctx, &m, x, x_dtype, in_stride, y, out_stride, tokens);
 }
 
 int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode) {
@@ -405,6 +451,36 @@ int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *
     if (host[1]) return fail(ctx, NUQ_NON_FINITE, "NonFiniteResult: a logit is not finite");
     *index = host[0];
     return NUQ_OK;
+}
+
+// Sampler.penalize on the device (backends/metal/ops/sampling.zig:63-71).
+int nuq_penalize(nuq_context *ctx, float *logits, uint64_t count, const uint32_t *history, uint64_t history_words,
+                 float repetition, float presence) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (!logits || !history) return fail(ctx, NUQ_INVALID_ARGUMENT, "null logits or history");
+    if (count == 0 || count > 0xffffffffull) return fail(ctx, NUQ_INVALID_SHAPE, "logit count out of range");
+    if (!std::isfinite(repetition) || repetition <= 0 || !std::isfinite(presence))
+        return fail(ctx, NUQ_INVALID_SHAPE, "penalties must be finite and the repetition positive");
+    if (history_words < (count + 31) / 32) return fail(ctx, NUQ_INVALID_SHAPE, "history shorter than the logits");
+    return hip_check(ctx, nuq::launch_penalize(ctx->stream, logits, (uint32_t)count, history, repetition, presence),
+                     "penalize launch");
+}
+
+// Backend.topk (backends/metal/ops/sampling.zig:44-57).
+int nuq_topk(nuq_context *ctx, const float *logits, uint64_t count, uint32_t k, float temperature,
+             const nuq_topk_buffers *out) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    if (!logits || !out || !out->values || !out->indices || !out->sums || !out->flags)
+        return fail(ctx, NUQ_INVALID_ARGUMENT, "null logits or top-k buffers");
+    if (count == 0 || count > nuq::TOPK_MAX_COUNT || k == 0 || k > nuq::TOPK_CAPACITY || k > count)
+        return fail(ctx, NUQ_INVALID_SHAPE, "top-k of %u over %llu logits is out of range", k,
+                    (unsigned long long)count);
+    if (!std::isfinite(temperature) || temperature <= 0)
+        return fail(ctx, NUQ_INVALID_SHAPE, "temperature must be finite and positive");
+    return hip_check(ctx,
+                     nuq::launch_topk(ctx->stream, logits, (uint32_t)count, k, temperature, ctx->topk_keys,
+                                      out->values, out->indices, out->sums, out->flags),
+                     "top-k launch");
 }
 
 // The tensor-data section of a GGUF file goes to the device unchanged

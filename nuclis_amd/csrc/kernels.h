@@ -47,6 +47,16 @@ hipError_t launch_rows(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
 hipError_t launch_segments(hipStream_t s, const SegmentsArgs &args, const float *x);
 int segment_rows_per_wave();
 hipError_t launch_argmax(hipStream_t s, const float *logits, uint64_t count, uint32_t *result);
+
+// Device sampling (sampling.hip). The partial top-k keeps at most
+// TOPK_CAPACITY entries of at most TOPK_MAX_COUNT logits and writes
+// TOPK_PARTIALS exp-sum partials (backends/metal/ops/sampling.zig:15-22).
+constexpr uint32_t TOPK_CAPACITY = 256, TOPK_PARTIALS = 64, TOPK_MAX_COUNT = TOPK_PARTIALS * 256 * 16;
+uint64_t topk_scratch_keys();
+hipError_t launch_penalize(hipStream_t s, float *logits, uint32_t count, const uint32_t *history, float repetition,
+                           float presence);
+hipError_t launch_topk(hipStream_t s, const float *logits, uint32_t count, uint32_t k, float temperature,
+                       uint64_t *scratch, float *values, uint32_t *indices, float *sums, uint32_t *flags);
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);

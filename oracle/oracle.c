@@ -318,3 +318,68 @@ int orc_argmax(const float *logits, size_t count, size_t *index) {
     *index = best;
     return ORC_OK;
 }
+
+/* Sampler.penalize (inference/src/sampling/root.zig:375-381) for every id:
+ * ids in the history bit set (bit id of word id / 32) get l / r for l > 0,
+ * else l * r, then minus presence; the others are copied. */
+int orc_penalize(const float *logits, size_t count, const uint32_t *history, size_t words, float repetition,
+                 float presence, float *out) {
+    if (count == 0 || words < (count + 31) / 32) return ORC_INVALID_SHAPE;
+    for (size_t i = 0; i < count; ++i) {
+        const float value = logits[i];
+        if (!(history[i / 32] & (1u << (i % 32)))) {
+            out[i] = value;
+            continue;
+        }
+        const float scaled = value > 0 ? value / repetition : value * repetition;
+        out[i] = scaled - presence;
+    }
+    return ORC_OK;
+}
+
+typedef struct {
+    uint32_t id;
+    float weight;
+} orc_candidate;
+
+/* Sampler.lessThan (sampling/root.zig:385-387): weight descending, id ascending. */
+static int orc_candidate_order(const void *pa, const void *pb) {
+    const orc_candidate *a = (const orc_candidate *)pa, *b = (const orc_candidate *)pb;
+    if (a->weight > b->weight) return -1;
+    if (a->weight < b->weight) return 1;
+    return a->id < b->id ? -1 : (a->id > b->id ? 1 : 0);
+}
+
+/* The readback a correct device produces (referenceTopK, sampling/root.zig:
+ * 701-715, with the device's non-finite rule of kernels/sampling.metal:58-67):
+ * the first k of the reference sort over the non-NaN logits, padded with
+ * (-inf, 0xffffffff) when fewer remain; total = sum over every logit of
+ * exp((l - max) / T) in F64 with max the first value; finite = no logit is
+ * NaN or infinite. */
+int orc_topk(const float *logits, size_t count, size_t k, float temperature, uint32_t *ids, float *values,
+             double *total, int *finite) {
+    if (count == 0 || k == 0 || k > count) return ORC_INVALID_SHAPE;
+    orc_candidate *c = (orc_candidate *)malloc(count * sizeof *c);
+    if (!c) return ORC_INVALID_SHAPE;
+    size_t n = 0;
+    int all_finite = 1;
+    for (size_t i = 0; i < count; ++i) {
+        if (!isfinite(logits[i])) all_finite = 0;
+        if (isnan(logits[i])) continue;
+        c[n].id = (uint32_t)i;
+        c[n].weight = logits[i];
+        ++n;
+    }
+    qsort(c, n, sizeof *c, orc_candidate_order);
+    for (size_t r = 0; r < k; ++r) {
+        ids[r] = r < n ? c[r].id : 0xffffffffu;
+        values[r] = r < n ? c[r].weight : -INFINITY;
+    }
+    const double maximum = values[0];
+    double sum = 0.0;
+    for (size_t i = 0; i < count; ++i) sum += exp(((double)logits[i] - maximum) / (double)temperature);
+    *total = sum;
+    *finite = all_finite;
+    free(c);
+    return ORC_OK;
+}

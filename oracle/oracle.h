@@ -24,6 +24,13 @@
  *                        for batched products (inference/metal-check.zig:4410-4424)
  *   orc_argmax           inference/src/sampling/root.zig:226-239 (first
  *                        maximum wins, a non-finite logit is an error)
+ *   orc_penalize         inference/src/sampling/root.zig:375-381 (penalize)
+ *                        over a history bit set (History.writeWords layout)
+ *   orc_topk             the readback referenceTopK builds
+ *                        (inference/src/sampling/root.zig:701-715: the
+ *                        Sampler.lessThan sort, F64 exp-sum) with the device
+ *                        rule that NaN never enters the list
+ *                        (backends/metal/kernels/sampling.metal:58-67)
  *
  * Every function is pinned by tests/test_oracle.py against the llama.cpp
  * fixtures the reference holds (tests/golden/), the reference's own
@@ -60,6 +67,10 @@ int orc_matmul(uint32_t encoding, size_t rows, size_t columns, const uint8_t *by
                const float *input, size_t in_stride, float *output, size_t out_stride, size_t tokens,
                int threads);
 int orc_argmax(const float *logits, size_t count, size_t *index);
+int orc_penalize(const float *logits, size_t count, const uint32_t *history, size_t words, float repetition,
+                 float presence, float *out);
+int orc_topk(const float *logits, size_t count, size_t k, float temperature, uint32_t *ids, float *values,
+             double *total, int *finite);
 int orc_default_threads(void);
 
 #ifdef __cplusplus

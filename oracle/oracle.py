@@ -59,6 +59,9 @@ def lib():
         L.orc_matvec.argtypes = [ctypes.c_uint32, c_sz, c_sz, c_p, c_sz, c_p, c_sz, c_p, c_sz, ctypes.c_int]
         L.orc_matmul.argtypes = [ctypes.c_uint32, c_sz, c_sz, c_p, c_sz, c_p, c_sz, c_p, c_sz, c_sz, ctypes.c_int]
         L.orc_argmax.argtypes = [c_p, c_sz, ctypes.POINTER(ctypes.c_size_t)]
+        L.orc_penalize.argtypes = [c_p, c_sz, c_p, c_sz, ctypes.c_float, ctypes.c_float, c_p]
+        L.orc_topk.argtypes = [c_p, c_sz, c_sz, ctypes.c_float, c_p, c_p, ctypes.POINTER(ctypes.c_double),
+                               ctypes.POINTER(ctypes.c_int)]
         _lib = L
     return _lib
 
@@ -129,6 +132,34 @@ def argmax(logits: np.ndarray) -> int:
     idx = ctypes.c_size_t(0)
     _check(lib().orc_argmax(_ptr(v), v.size, ctypes.byref(idx)))
     return idx.value
+
+
+def penalize(logits: np.ndarray, history_words: np.ndarray, repetition: float, presence: float) -> np.ndarray:
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    h = np.ascontiguousarray(history_words, dtype=np.uint32)
+    out = np.empty_like(v)
+    _check(lib().orc_penalize(_ptr(v), v.size, _ptr(h), h.size, repetition, presence, _ptr(out)))
+    return out
+
+
+def topk(logits: np.ndarray, k: int, temperature: float):
+    """(ids uint32[k], values float32[k], total F64, finite)."""
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.empty(k, dtype=np.uint32)
+    vals = np.empty(k, dtype=np.float32)
+    total = ctypes.c_double(0)
+    finite = ctypes.c_int(0)
+    _check(lib().orc_topk(_ptr(v), v.size, k, temperature, _ptr(ids), _ptr(vals), ctypes.byref(total),
+                          ctypes.byref(finite)))
+    return ids, vals, total.value, bool(finite.value)
+
+
+def history_words(ids, count: int) -> np.ndarray:
+    """History.writeWords layout (sampling/root.zig): bit id of word id / 32."""
+    words = np.zeros((count + 31) // 32, dtype=np.uint32)
+    for i in ids:
+        words[i // 32] |= np.uint32(1 << (i % 32))
+    return words
 
 
 def default_threads() -> int:

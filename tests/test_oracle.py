@@ -10,6 +10,7 @@ Sources of truth, none of them a retyping of the oracle's formulas:
   * brute-force F64 sums for matvec.
 """
 import json
+import math
 from pathlib import Path
 
 import numpy as np
@@ -311,3 +312,78 @@ def test_argmax_first_maximum_and_non_finite():
         orc.argmax(np.array([1, np.inf], np.float32))
     with pytest.raises(orc.OracleError, match="NonFinite"):
         orc.argmax(np.array([np.nan, 1], np.float32))
+
+
+# -- device sampling oracles (penalize, top-k) ------------------------------------------
+
+
+def test_penalize_oracle_hand_computed_cases():
+    """sampling/root.zig:541-611: history {1, 3} over [1.0, 2.0, 1.5, -1.0]."""
+    logits = np.array([1.0, 2.0, 1.5, -1.0], np.float32)
+    words = orc.history_words([1, 3], 4)
+    assert words[0] == (1 << 1) | (1 << 3)
+    assert orc.penalize(logits, words, 1.0, 1.0).tolist() == [1.0, 1.0, 1.5, -2.0]   # presence 1.0
+    assert orc.penalize(logits, words, 1.0, 0.5).tolist() == [1.0, 1.5, 1.5, -1.5]   # presence 0.5
+    assert orc.penalize(logits, words, 2.0, 0.0).tolist() == [1.0, 1.0, 1.5, -2.0]   # repetition 2.0
+    # repetition first, then presence: 2/4 - 1 = -0.5 and -1*4 - 1 = -5
+    assert orc.penalize(logits, words, 4.0, 1.0).tolist() == [1.0, -0.5, 1.5, -5.0]
+    only3 = orc.history_words([3], 4)
+    assert orc.penalize(logits, only3, 1.0, -5.0).tolist() == [1.0, 2.0, 1.5, 4.0]   # rewarding presence
+    tiny = orc.history_words([0], 2)
+    assert np.isinf(orc.penalize(np.array([1e30, 0], np.float32), tiny, 1e-40, 0.0)[0])
+    with pytest.raises(orc.OracleError):
+        orc.penalize(logits, np.zeros(0, np.uint32), 1.0, 0.0)
+
+
+def test_history_words_layout():
+    """History.writeWords (sampling/root.zig:133-140, test :530-531)."""
+    assert orc.history_words([3, 9], 16)[0] == (1 << 3) | (1 << 9)
+    w = orc.history_words([31, 32, 95], 96)
+    assert w.tolist() == [1 << 31, 1, 1 << 31]
+
+
+def _lexsort_topk(v, k):
+    """Independent restatement: numpy's lexsort on (id, -value) over the
+    non-NaN entries, padded with (-inf, 0xffffffff)."""
+    ids = np.arange(v.size)
+    keep = ~np.isnan(v)
+    order = np.lexsort((ids[keep], -v[keep].astype(np.float64)))
+    top = ids[keep][order][:k]
+    vals = v[top]
+    pad = k - top.size
+    return (np.concatenate([top, np.full(pad, 0xffffffff)]).astype(np.uint32),
+            np.concatenate([vals, np.full(pad, -np.inf, np.float32)]).astype(np.float32))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_oracle_matches_an_independent_sort_and_fsum(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(300, 5000))
+    v = (rng.standard_normal(n) * 3).astype(np.float32)
+    v[rng.integers(0, n, 40)] = 2.5                          # ties
+    v[rng.integers(0, n, 5)] = 0.0
+    v[rng.integers(0, n, 5)] = -0.0                          # -0 ties with +0
+    v[rng.integers(0, n, 3)] = -np.inf
+    if seed % 2:
+        v[rng.integers(0, n, 7)] = np.nan
+    k = int(rng.integers(1, 257))
+    t = float(rng.choice([0.7, 1.0, 1.5]))
+    ids, vals, total, finite = orc.topk(v, k, t)
+    want_ids, want_vals = _lexsort_topk(v, k)
+    assert ids.tolist() == want_ids.tolist()
+    assert vals.view(np.uint32).tolist() == want_vals.view(np.uint32).tolist()
+    m = float(vals[0])
+    exact = math.fsum(math.exp((float(x) - m) / t) for x in v.astype(np.float64))
+    if finite:
+        assert abs(total - exact) <= 1e-12 * exact
+    else:
+        assert math.isnan(total) or not np.all(np.isfinite(v))
+    assert finite == bool(np.all(np.isfinite(v)))
+
+
+def test_topk_oracle_pads_when_nan_leaves_fewer_than_k():
+    v = np.array([np.nan, 1.0, np.nan, -np.inf], np.float32)
+    ids, vals, _, finite = orc.topk(v, 4, 1.0)
+    assert ids.tolist() == [1, 3, 0xffffffff, 0xffffffff]
+    assert vals[:2].tolist() == [1.0, -np.inf] and np.all(np.isneginf(vals[2:]))
+    assert not finite
