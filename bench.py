@@ -218,6 +218,26 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
             "frac_f16_peak": flops / s / 1e12 / F16_PEAK_TFLOPS}
 
 
+def bench_library_gemm(torch, stream, rows, columns, tokens, reps=20, warmup=3):
+    """Context for the prefill roofline: torch's f16 GEMM (hipBLASLt) on the
+    same M x N x K with f16 operands already in HBM -- no dequantization and
+    F16 output, so it is an upper reference for the fused kernel, not a
+    product path."""
+    a = torch.randn(tokens, columns, device="cuda", dtype=torch.float16)
+    b = torch.randn(rows, columns, device="cuda", dtype=torch.float16)
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            c = a @ b.T
+        torch.cuda.synchronize()
+        with Timer(torch, stream) as t:
+            for _ in range(reps):
+                c = a @ b.T
+    del c
+    s = t.ms / 1e3 / reps
+    return {"ms": s * 1e3, "tflops": 2.0 * tokens * rows * columns / s / 1e12}
+
+
 def bench_layer(torch, nq, backend, stream, reps=20):
     """Configuration 3: one decode step (q/k/v, o, gate/up, down Q4_K + Q6_K
     lm_head, M=1) captured as a HIP graph; GB/s of weight bytes per step."""
@@ -310,6 +330,7 @@ def main():
     prefill = None
     if not only or "prefill" in only:
         prefill = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 4096)
+        prefill["library"] = bench_library_gemm(torch, stream, 17408, 5120, 4096)
     extras = {}
     if args.extras:
         extras["q4k_down_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q4_K, 5120, 17408,
@@ -368,7 +389,8 @@ def main():
                              "tflops": round(prefill["tflops"], 2), "ms": round(prefill["ms"], 4),
                              "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
                                           "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                          "frac": round(prefill["frac_f16_peak"], 4)}}
+                                          "frac": round(prefill["frac_f16_peak"], 4)},
+                             "library_f16_gemm_same_shape_tflops": round(prefill["library"]["tflops"], 2)}
     if extras:
         result["extras"] = extras
     backend.close()
