@@ -964,50 +964,75 @@ struct VLane<8> {
 
 constexpr int VF_MAX_WAVES = 16;
 
-template <uint32_t ENC, typename XT>
+// RG row groups of 16 per wave: the x fragments of a block are loaded once
+// and feed RG MFMA chains, so a workgroup reads x once per 16*RG rows.
+template <uint32_t ENC, typename XT, int RG>
 __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                     uint32_t rows, uint32_t nblocks,
                                                                     const XT *__restrict__ x, uint64_t in_stride,
                                                                     float *__restrict__ y, uint64_t out_stride,
                                                                     uint32_t tokens) {
-    __shared__ float part_sums[VF_MAX_WAVES][16][16];
+    __shared__ float part_sums[VF_MAX_WAVES][RG][16][16];
     using L = VLane<ENC>;
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t r16 = lane & 15, h = lane >> 4;
-    const uint32_t row0 = blockIdx.x * 16;
-    const uint8_t *wrow = w + (uint64_t)min(row0 + r16, rows - 1) * stride;
+    const uint32_t row0 = blockIdx.x * 16 * RG;
     const bool tok_ok = r16 < tokens;
     const XT *xrow = x + (uint64_t)(tok_ok ? r16 : 0) * in_stride;
 
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    floatx4 acc[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = wv; b < nblocks; b += nwaves) {
-        half8 a[8];
-        L::dequant(wrow + (uint64_t)b * L::BLOCK_BYTES, h, a);
+        half8 bx[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            half8 bx;
             const uint32_t col = b * L::BLOCK_VALUES + L::col(h, c);
             if constexpr (sizeof(XT) == 2) {
-                bx = tok_ok ? *(const half8 *)((const _Float16 *)xrow + col) : half8{};
+                bx[c] = tok_ok ? *(const half8 *)((const _Float16 *)xrow + col) : half8{};
             } else {
                 float4 f0 = tok_ok ? *(const float4 *)((const float *)xrow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
                 float4 f1 = tok_ok ? *(const float4 *)((const float *)xrow + col + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                bx[0] = (_Float16)f0.x; bx[1] = (_Float16)f0.y; bx[2] = (_Float16)f0.z; bx[3] = (_Float16)f0.w;
-                bx[4] = (_Float16)f1.x; bx[5] = (_Float16)f1.y; bx[6] = (_Float16)f1.z; bx[7] = (_Float16)f1.w;
+                bx[c][0] = (_Float16)f0.x; bx[c][1] = (_Float16)f0.y; bx[c][2] = (_Float16)f0.z; bx[c][3] = (_Float16)f0.w;
+                bx[c][4] = (_Float16)f1.x; bx[c][5] = (_Float16)f1.y; bx[c][6] = (_Float16)f1.z; bx[c][7] = (_Float16)f1.w;
             }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], bx, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            const uint8_t *wrow = w + (uint64_t)min(row0 + 16 * g + r16, rows - 1) * stride;
+            half8 a[8];
+            L::dequant(wrow + (uint64_t)b * L::BLOCK_BYTES, h, a);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], bx[c], acc[g], 0, 0, 0);
         }
     }
     // D layout: lane l holds token l%16, rows 4*(l/16) + i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part_sums[wv][4 * h + i][r16] = acc[i];
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part_sums[wv][g][4 * h + i][r16] = acc[g][i];
     __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < 256; idx += blockDim.x) {
-        const uint32_t rr = idx >> 4, t = idx & 15;
+    for (uint32_t idx = threadIdx.x; idx < 256 * RG; idx += blockDim.x) {
+        const uint32_t g = idx >> 8, rr = (idx >> 4) & 15, t = idx & 15;
         float v = 0.f;
-        for (uint32_t k = 0; k < nwaves; ++k) v += part_sums[k][rr][t];
-        if (t < tokens && row0 + rr < rows) y[(uint64_t)t * out_stride + row0 + rr] = v;
+        for (uint32_t k = 0; k < nwaves; ++k) v += part_sums[k][g][rr][t];
+        const uint32_t row = row0 + 16 * g + rr;
+        if (t < tokens && row < rows) y[(uint64_t)t * out_stride + row] = v;
     }
+}
+
+template <uint32_t ENC, int RG>
+static hipError_t launch_verify_rg(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
+                                   uint32_t waves, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                                   uint64_t out_stride, uint32_t tokens) {
+    dim3 grid((rows + 16 * RG - 1) / (16 * RG)), block(64 * waves);
+    if (x_f16)
+        hipLaunchKernelGGL((verify_kernel<ENC, _Float16, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                           (const _Float16 *)x, in_stride, y, out_stride, tokens);
+    else
+        hipLaunchKernelGGL((verify_kernel<ENC, float, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                           (const float *)x, in_stride, y, out_stride, tokens);
+    return hipGetLastError();
 }
 
 template <uint32_t ENC>
@@ -1015,18 +1040,15 @@ static hipError_t launch_verify_enc(hipStream_t s, const uint8_t *w, uint64_t st
                                     uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                     uint64_t out_stride, uint32_t tokens) {
     const uint32_t nblocks = columns / 256;
-    // waves: as few as keep the per-wave block count at its minimum
-    // ceil(nblocks / 16), so the blocks split as evenly as possible
-    const uint32_t per_wave = (nblocks + VF_MAX_WAVES - 1) / VF_MAX_WAVES;
+    // About five blocks per wave (at most VF_MAX_WAVES waves), split evenly:
+    // measured best at K = 5120 (4 waves) and K = 17408 (14 waves).
+    const uint32_t per_wave = std::max(5u, (nblocks + VF_MAX_WAVES - 1) / VF_MAX_WAVES);
     const uint32_t waves = (nblocks + per_wave - 1) / per_wave;
-    dim3 grid((rows + 15) / 16), block(64 * waves);
-    if (x_f16)
-        hipLaunchKernelGGL((verify_kernel<ENC, _Float16>), grid, block, 0, s, w, stride, rows, nblocks,
-                           (const _Float16 *)x, in_stride, y, out_stride, tokens);
-    else
-        hipLaunchKernelGGL((verify_kernel<ENC, float>), grid, block, 0, s, w, stride, rows, nblocks,
-                           (const float *)x, in_stride, y, out_stride, tokens);
-    return hipGetLastError();
+    // Two row groups per wave halve the x reads once there are enough rows
+    // to keep 160 or more workgroups.
+    if (rows >= 32u * 160)
+        return launch_verify_rg<ENC, 2>(s, w, stride, rows, nblocks, waves, x, x_f16, in_stride, y, out_stride, tokens);
+    return launch_verify_rg<ENC, 1>(s, w, stride, rows, nblocks, waves, x, x_f16, in_stride, y, out_stride, tokens);
 }
 
 template <uint32_t ENC>
