@@ -120,3 +120,13 @@ def test_quantizer_refusals():
         nq.quantize(12, np.zeros((2, 100), np.float32))
     with pytest.raises(nq.UnsupportedTensorEncoding):
         nq.quantize(3, np.zeros((2, 256), np.float32))
+
+
+def test_c_abi_host_checks_from_c():
+    """tests/c_abi/nuq_check.c's host-only part (GGUF parsing through the C
+    header), linked against libnuq.so without touching a GPU."""
+    import subprocess
+    exe = ROOT / "tests" / "c_abi" / "_build" / "nuq_check"
+    assert exe.exists(), "run __graft_entry__.build()"
+    r = subprocess.run([str(exe), "--host-only"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "host OK" in r.stdout, r.stdout + r.stderr
