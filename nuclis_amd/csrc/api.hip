@@ -117,13 +117,14 @@ int gemv_rows_per_wave(uint32_t encoding, uint64_t rows) {
     return rows >= 8192 ? 4 : 2;
 }
 
-// The decode GEMV: Q4_K on the integer-dot K-split kernel, the other
-// encodings on the row-per-wave kernels.
+// The decode GEMV: every encoding on the integer-dot DMA kernel where its
+// shape fits (Q8_0 needs K % 256 == 0), else the register kernel (Q4_K), the
+// row-per-wave kernels (Q6_K, Q8_0) or the generic kernel (Q5_K, IQ4_XS).
 int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, float *out) {
-    if (m->encoding == NUQ_Q6_K) {
+    if (m->encoding == NUQ_Q6_K || m->encoding == NUQ_Q8_0) {
         hipError_t e = nuq::launch_gemv_dma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
                                             (uint32_t)m->rows, (uint32_t)m->columns, x, out);
-        if (e != hipErrorInvalidValue) return hip_check(ctx, e, "q6_k gemv launch");
+        if (e != hipErrorInvalidValue) return hip_check(ctx, e, "gemv launch");
     }
     if (m->encoding == NUQ_Q5_K || m->encoding == NUQ_IQ4_XS) {
         hipError_t e = nuq::launch_gemv_dma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,

@@ -569,6 +569,65 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
 };
 
 template <>
+struct GdEnc<8> {  // Q8_0: eight 34-byte blocks (256 values) as one unit; lane j: blocks 2j, 2j+1
+    static constexpr uint32_t BYTES = 272, INSTRS = (BYTES + 63) / 64;
+    uint32_t qa[8], qb[8], da, db;
+    // The pair's 68 bytes start 4-byte aligned (units are 16-byte aligned in
+    // the ring, 68j into the unit): block 2j's codes sit 2 bytes in and are
+    // shifted into dwords with v_alignbyte_b32; block 2j+1's are aligned.
+    template <int VM>
+    __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        const uint32_t a = lds_u8_addr(blk) + 68 * j;
+        u32x2_t q[8];
+        uint32_t last;
+        asm volatile(
+            "s_waitcnt vmcnt(%9)\n\t"
+            "ds_read2_b32 %0, %10 offset1:1\n\t"
+            "ds_read2_b32 %1, %10 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %2, %10 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %3, %10 offset0:6 offset1:7\n\t"
+            "ds_read2_b32 %4, %10 offset0:8 offset1:9\n\t"
+            "ds_read2_b32 %5, %10 offset0:10 offset1:11\n\t"
+            "ds_read2_b32 %6, %10 offset0:12 offset1:13\n\t"
+            "ds_read2_b32 %7, %10 offset0:14 offset1:15\n\t"
+            "ds_read_b32 %8, %10 offset:64\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]),
+              "=&v"(q[7]), "=&v"(last)
+            : "n"(VM), "v"(a)
+            : "memory");
+        uint32_t r[17];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            r[2 * k] = q[k].x;
+            r[2 * k + 1] = q[k].y;
+        }
+        r[16] = last;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qa[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], 2);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qb[k] = r[9 + k];
+        da = r[0] & 0xffffu;
+        db = r[8] >> 16;
+    }
+    // w = d * q per 32-value block (quant/decode.zig:57-63): the exact
+    // integer sums of q * x16 scaled by d and the slice scale in F32
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t, uint32_t, bool) const {
+        int ah = 0, al = 0, bh = 0, bl = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            ah = dot4(qa[k], A.hi[k], ah);
+            al = dot4(qa[k], A.lo[k], al);
+            bh = dot4(qb[k], B.hi[k], bh);
+            bl = dot4(qb[k], B.lo[k], bl);
+        }
+        const float ta = half_bits(da) * A.scale, tb = half_bits(db) * B.scale;
+        return fmaf(ta, (float)(ah * 256 + al), tb * (float)(bh * 256 + bl));
+    }
+};
+
+template <>
 struct GdEnc<23> {  // IQ4_XS: 8-byte header + the pair's 32 code bytes (8-byte aligned)
     static constexpr uint32_t BYTES = 136, INSTRS = (BYTES + 63) / 64;
     uint32_t h0, h1;
@@ -811,9 +870,15 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     // last step), so the grid is the CU count and each CU streams the same
     // share of the bytes.
     const uint32_t rows_per_wg = std::max(1u, (rows + cus - 1) / cus);
+    // Fewer wave sets when the rings, x slices and partials exceed the LDS.
+    auto lds_for = [&](uint32_t st) {
+        const size_t wv = (size_t)set_waves * st;
+        return wv * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
+               ((size_t)rows_per_wg * set_waves + wv) * 4;
+    };
+    while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
     const uint32_t waves = set_waves * sets;
-    const size_t lds = (size_t)waves * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
-                       ((size_t)rows_per_wg * set_waves + waves) * 4;
+    const size_t lds = lds_for(sets);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
     hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)),
@@ -903,6 +968,9 @@ hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, u
         // copy reads up to 8 bytes past it: the next row for all but the
         // matrix's last row, which an extra workgroup computes directly.
         return launch_dma<14, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1, nblocks * 210u % 16 != 0);
+    if (encoding == 8 && columns % 256 == 0)  // nblocks counts 256-value units of eight Q8_0 blocks
+        return four ? launch_dma<8, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
+                    : launch_dma<8, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);
     if (encoding == 23 && nblocks % 2 == 0)
         return four ? launch_dma<23, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
                     : launch_dma<23, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);

@@ -19,7 +19,7 @@ from tests.gpu_util import check_close, mass, to_gpu, xq_mass
 
 pytestmark = pytest.mark.gpu
 
-INT_GEMV = {12, 13, 14, 23}
+INT_GEMV = {8, 12, 13, 14, 23}
 SPECS = [("blk.0.attn_q.weight", 12, 512, 2048), ("blk.0.ffn_down.weight", 14, 256, 2560),
          ("blk.0.attn_v.weight", 8, 296, 1024), ("blk.0.ffn_up.weight", 13, 256, 1280),
          ("blk.0.ffn_gate.weight", 23, 384, 2048)]

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "decoder_fixtures.json").read_text())
 F32_K = 4e-6   # reference matvec bound (metal-check.zig:3976)
-INT_GEMV = {12, 13, 14, 23}  # encodings whose M=1 GEMV runs on the integer-dot kernels
+INT_GEMV = {8, 12, 13, 14, 23}  # encodings whose M=1 GEMV runs on the integer-dot kernels
 F16_K = 2e-3   # f16-rounded operands
 
 
