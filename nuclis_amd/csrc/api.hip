@@ -388,6 +388,9 @@ int nuq_gemm(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride
     return nuq_matmul(ctx, &m, x, x_dtype, in_stride, y, out_stride, tokens);
 }
 
+// Rows from which a SiLU pair runs as two decode GEMVs plus the epilogue.
+constexpr uint64_t PAIR_SPLIT_ROWS = 4096;
+
 int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode) {
     if (!ctx) return NUQ_INVALID_ARGUMENT;
     if (!segments || count == 0 || count > 4) return fail(ctx, NUQ_INVALID_SHAPE, "segments: 1..4 projections");
@@ -433,6 +436,20 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
         waves += (uint32_t)((m.rows + rpw - 1) / rpw);
     }
     args.wave_start[count] = waves;
+    // A large SiLU pair streams faster as two decode GEMVs (gate into the
+    // output, up into the prefill workspace, which no GEMV uses) and the
+    // elementwise epilogue than as one merged row-per-wave pass.
+    if (mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only && segments[0].matrix.rows >= PAIR_SPLIT_ROWS &&
+        segments[0].matrix.rows * sizeof(float) <= (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float)) {
+        const nuq_matrix &g = segments[0].matrix, &u = segments[1].matrix;
+        float *up = ctx->split.work;
+        int e = run_gemv(ctx, &g, g.byte_len / g.rows, x, segments[0].output);
+        if (e) return e;
+        e = run_gemv(ctx, &u, u.byte_len / u.rows, x, up);
+        if (e) return e;
+        return hip_check(ctx, nuq::launch_silu_mul(ctx->stream, segments[0].output, up, (uint32_t)g.rows),
+                         "silu pair epilogue");
+    }
     if (mode != NUQ_SEGMENT_PLAIN) args.wave_start[1] = (uint32_t)((segments[0].matrix.rows + rpw - 1) / rpw);
     return hip_check(ctx, nuq::launch_segments(ctx->stream, args, x), "segments launch");
 }

@@ -764,4 +764,20 @@ hipError_t launch_argmax(hipStream_t s, const float *logits, uint64_t count, uin
     return hipGetLastError();
 }
 
+// The SiLU pair epilogue over two finished products: out[r] = silu(out[r])
+// * up[r], with the segments kernel's silu (cpu/vector.zig:178-181).
+__global__ void __launch_bounds__(256) silu_mul_kernel(float *__restrict__ out, const float *__restrict__ up,
+                                                       uint32_t n) {
+    const uint32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= n) return;
+    const float g = out[r];
+    const float silu = (g == -INFINITY) ? -0.f : g / (1.f + expf(-g));
+    out[r] = silu * up[r];
+}
+
+hipError_t launch_silu_mul(hipStream_t s, float *out, const float *up, uint32_t n) {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, out, up, n);
+    return hipGetLastError();
+}
+
 }  // namespace nuq

@@ -47,6 +47,7 @@ hipError_t launch_rows(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
 hipError_t launch_segments(hipStream_t s, const SegmentsArgs &args, const float *x);
 int segment_rows_per_wave();
 hipError_t launch_argmax(hipStream_t s, const float *logits, uint64_t count, uint32_t *result);
+hipError_t launch_silu_mul(hipStream_t s, float *out, const float *up, uint32_t n);
 
 // Device sampling (sampling.hip). The partial top-k keeps at most
 // TOPK_CAPACITY entries of at most TOPK_MAX_COUNT logits and writes

@@ -359,6 +359,36 @@ def test_segments_plain_and_silu_pair(backend):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("rows", [4096, 17408])
+def test_silu_pair_large_runs_as_two_gemvs(backend, rows):
+    """From 4096 rows the pair runs as two decode GEMVs plus the epilogue:
+    the integer-dot bound (F32 plus the x-rounding term) propagated through
+    silu(g) * u (|silu'| <= 1.1, |silu(g)| <= |g|), and the result equal to
+    the epilogue applied to the two GEMVs alone."""
+    import torch
+    columns = 5120
+    x = gaussian(42, columns)
+    xg = to_gpu(x)
+    gate, up = quantized(12, rows, columns, 52), quantized(12, rows, columns, 53)
+    mg_, mu_ = nq.Matrix(12, rows, columns, to_gpu(gate)), nq.Matrix(12, rows, columns, to_gpu(up))
+    pair_out = torch.full((rows,), np.nan, device="cuda")
+    backend.matvec_segments([(mg_, pair_out), (mu_, pair_out)], xg, nq.SEGMENT_SILU_MUL_PAIR)
+    gd, ud = torch.empty(rows, device="cuda"), torch.empty(rows, device="cuda")
+    backend.matvec(mg_, xg, gd)
+    backend.matvec(mu_, xg, ud)
+    backend.sync()
+    got = pair_out.cpu().numpy().astype(np.float64)
+    gg, uu = gd.cpu().numpy().astype(np.float64), ud.cpu().numpy().astype(np.float64)
+    assert np.allclose(got, gg / (1 + np.exp(-gg)) * uu, rtol=1e-6, atol=1e-12)
+    g = orc.matvec(12, rows, columns, gate, x).astype(np.float64)
+    u = orc.matvec(12, rows, columns, up, x).astype(np.float64)
+    want = g / (1 + np.exp(-g)) * u
+    eg = F32_K * mass(12, gate, rows, columns, x)[0] + xq_mass(12, gate, rows, columns, x)[0] + 1e-6
+    eu = F32_K * mass(12, up, rows, columns, x)[0] + xq_mass(12, up, rows, columns, x)[0] + 1e-6
+    bound = 1.1 * np.abs(u) * eg + (np.abs(g) + eg) * eu + 1e-6 * np.abs(want) + 1e-6
+    assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
+
+
 def segments_plain(backend, shapes):
     import torch
     columns = 5120
