@@ -462,6 +462,16 @@ struct WRaw<8> {
 
 constexpr int PF_BM = 256, PF_BN = 256, PF_GROUP_M = 4;
 
+// Step order per encoding, measured at M = 4096 on 17408x5120 and
+// 5120x17408: issuing the activation copy before the weight prefetch and
+// ending the step with explicit waits and a fence-free barrier gains 8 %
+// (Q8_0), 7 % (Q6_K) and 2 % (Q5_K); Q4_K and IQ4_XS lose 2-2.5 % and keep
+// the prefetch-first order with __syncthreads. Bit e of the mask is encoding e.
+#ifndef NUQ_PF_COPY_FIRST_MASK
+#define NUQ_PF_COPY_FIRST_MASK ((1u << 8) | (1u << 13) | (1u << 14))
+#endif
+template <uint32_t ENC> struct PF_COPY_FIRST { static constexpr bool value = (NUQ_PF_COPY_FIRST_MASK >> (ENC & 31)) & 1u; };
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
 
@@ -620,7 +630,9 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
         half8 fa[2][4], fb[2][TJ];                                                                                 \
         _Pragma("unroll") for (int i = 0; i < 4; ++i) fa[0][i] = *(const half8 *)(xa + i * 32 * LDS_PITCH);        \
         _Pragma("unroll") for (int j = 0; j < (int)TJ; ++j) fb[0][j] = *(const half8 *)(wb + j * 32 * LDS_PITCH);  \
-        if (ks_ + 2 < ksteps) {                                                                                    \
+        const bool far_ = ks_ + 2 < ksteps;                                                                        \
+        /* PF_COPY_FIRST: the activation copy is issued before the weight prefetch */                            \
+        if (!PF_COPY_FIRST<ENC>::value && far_) {                                                                  \
             _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) WFAR[s_].load(wrow, ks_ + 2, NUQ_PF_PART(s_));  \
         }                                                                                                          \
         if (next) {                                                                                                \
@@ -630,6 +642,9 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
                 _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_)                                             \
                     xr[s_].load(xrow + NUQ_PF_PART(s_) * 32 + (ks_ + 1) * BK, xvalid);                             \
             }                                                                                                      \
+        }                                                                                                          \
+        if (PF_COPY_FIRST<ENC>::value && far_) {                                                                   \
+            _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) WFAR[s_].load(wrow, ks_ + 2, NUQ_PF_PART(s_));  \
         }                                                                                                          \
         _Pragma("unroll") for (uint32_t kk = 0; kk < BK / 16; ++kk) {                                              \
             const uint32_t p_ = kk & 1;                                                                            \
@@ -651,8 +666,15 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
                 _Pragma("unroll") for (uint32_t c = 0; c < 4; ++c) xr[s_].store(xdst, c);                          \
             }                                                                                                      \
         }                                                                                                          \
-        if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70); /* vmcnt(0): this step's DMA has landed */         \
-        __syncthreads();                                                                                           \
+        if (DMA && PF_COPY_FIRST<ENC>::value) {                                                                    \
+            /* this step's copies have landed and the dequantised weights are written; the barrier */             \
+            /* carries no fence */                                                                                \
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");                                         \
+            __builtin_amdgcn_s_barrier();                                                                          \
+        } else {                                                                                                   \
+            if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70); /* vmcnt(0): this step's DMA has landed */     \
+            __syncthreads();                                                                                       \
+        }                                                                                                          \
     }
     for (uint32_t ks = 0; ks < ksteps; ++ks) {
         NUQ_PF_STEP(ks, wA, wB)
