@@ -363,7 +363,6 @@ struct WRaw<14> {
 };
 template <>
 struct WRaw<13> {
-    static constexpr uint32_t MIN_LOADS = 3;
     uint4 hdr, qh, qs;
     uint32_t p2;  // 2 * pair: the high-plane bit of the low-nibble group
     float mul0, off0, mul1, off1;
@@ -406,7 +405,6 @@ struct WRaw<13> {
 };
 template <>
 struct WRaw<23> {
-    static constexpr uint32_t MIN_LOADS = 3;
     uint2 hdr, q01, q23;  // d, scales_h, scales_l; the group's 16 code bytes
     float mul;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {

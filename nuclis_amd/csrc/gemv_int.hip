@@ -413,7 +413,7 @@ struct GdEnc<12> {  // Q4_K: header + the pair's 32 code bytes
             : "n"(VM), "v"(a), "v"(b)
             : "memory");
     }
-    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t shift,
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t, uint32_t shift,
                                          bool direct) const {
         return q4k_lane(make_uint4(h.x, h.y, h.z, h.w), make_uint4(q0.x, q0.y, q0.z, q0.w),
                         make_uint4(q1.x, q1.y, q1.z, q1.w), A, B, shift, direct);

@@ -183,7 +183,7 @@ struct Cursor {
     }
     int kind(uint32_t *t) {
         NUQ_TRY(integer(t));
-        return *t <= NUQ_GGUF_FLOAT64 ? NUQ_OK : NUQ_GGUF_INVALID_METADATA_TYPE;
+        return *t <= NUQ_GGUF_FLOAT64 ? (int)NUQ_OK : (int)NUQ_GGUF_INVALID_METADATA_TYPE;
     }
     int value(uint32_t tag, bool retain, nuq::GgufValue *v);
 };

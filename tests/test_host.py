@@ -130,3 +130,18 @@ def test_c_abi_host_checks_from_c():
     assert exe.exists(), "run __graft_entry__.build()"
     r = subprocess.run([str(exe), "--host-only"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0 and "host OK" in r.stdout, r.stdout + r.stderr
+
+
+def test_gguf_reader_survives_corruption_under_sanitizers():
+    """tests/c_abi/gguf_fuzz.c: the GGUF reader (host C++) built on its own
+    with AddressSanitizer and UBSan, fed every truncation, every byte/u32/u64
+    patch and 200,000 random edits of the reference's wire fixture
+    (gguf.zig:617-650). Any overread, leak or undefined behaviour fails."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("no host C++ compiler")
+    d = ROOT / "tests" / "c_abi"
+    subprocess.run(["make", "-s", "-C", str(d), "fuzz"], check=True, capture_output=True, timeout=300)
+    r = subprocess.run([str(d / "_build" / "gguf_fuzz")], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "gguf_fuzz: OK" in r.stdout, r.stdout + r.stderr
