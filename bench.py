@@ -201,17 +201,19 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
     w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
     x = torch.from_numpy(gaussian(7, (tokens, columns))).cuda().to(torch.float16)
     wg = torch.from_numpy(w).cuda()
-    m = nq.Matrix(encoding, rows, columns, wg)
+    # rotating weight copies (>= 512 MB), so every launch streams from HBM
+    # and not from the 256 MB last-level cache
+    mats = [nq.Matrix(encoding, rows, columns, wg if i == 0 else wg.clone()) for i in range(copies_for(w.nbytes))]
     y = torch.empty((tokens, rows), device="cuda")
     k = nq.KERNEL_TILE if kernel is None else kernel
     stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
+        for i in range(warmup):
+            backend.matmul_kernel(k, mats[i % len(mats)], x, columns, y, rows, tokens)
         torch.cuda.synchronize()
         with Timer(torch, stream) as t:
-            for _ in range(reps):
-                backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
+            for i in range(reps):
+                backend.matmul_kernel(k, mats[i % len(mats)], x, columns, y, rows, tokens)
     s = t.ms / 1e3 / reps
     flops = 2.0 * tokens * rows * columns
     return {"ms": s * 1e3, "tflops": flops / s / 1e12, "flops": flops, "weight_gbs": w.nbytes / s / 1e9,
@@ -356,6 +358,10 @@ def main():
             for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
                 extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120,
                                                                    8, reps=200, warmup=20, kernel=kid)
+            extras["verify_m8_q4k_down_tile"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 5120, 17408, 8,
+                                                           reps=200, warmup=20)
+            extras["verify_m8_q5k_gate_tile"] = bench_gemm(torch, nq, backend, stream, nq.Q5_K, 17408, 5120, 8,
+                                                           reps=200, warmup=20)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(g["w"], x_host, rows, columns, args.cpu_seconds)

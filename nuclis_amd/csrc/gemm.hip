@@ -982,6 +982,161 @@ struct VLane<8> {
     }
 };
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two f16 values 1024 + v from bytes i and j of t (each v < 1024): the
+// byte goes into the low mantissa byte of 1024.0 (0x6400, ulp 1) by one
+// v_perm_b32 whose second source supplies the 0x64 exponent bytes.
+template <int I, int J>
+__device__ __forceinline__ half2v f16_biased(uint32_t t) {
+    constexpr uint32_t sel = (uint32_t)I | (4u << 8) | ((uint32_t)J << 16) | (4u << 24);
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, t, sel));
+}
+
+// (1024 + v) * s - 1024 * s, fused (v_pk_fma_f16): v * s rounded once, and
+// exact when |v * s| <= 2048.
+__device__ __forceinline__ uint32_t scaled_codes(half2v biased, half2v s, half2v c) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(biased, s, c));
+}
+
+// Six-bit scales and minima of Q4_K groups 2h and 2h+1 (the 12 scale bytes
+// in s0, s1, s2; quant/decode.zig:155-158) without a branch on h: both
+// groups sit in adjacent bytes 2(h&1), 2(h&1)+1 of each word, so the byte
+// pairs are combined at once and the h >= 2 form is selected. Returns
+// (sc0 | sc1 << 8) in *sc and (m0 | m1 << 8) in *m.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t h, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t *sc,
+                                                   uint32_t *m) {
+    const uint32_t sh = 16 * (h & 1);
+    const uint32_t b0 = s0 >> sh, b1 = s1 >> sh, b2 = s2 >> sh;
+    const uint32_t sc_lo = b0 & 0x3f3fu, m_lo = b1 & 0x3f3fu;
+    const uint32_t sc_hi = (b2 & 0x0f0fu) | ((b0 >> 2) & 0x3030u);
+    const uint32_t m_hi = ((b2 >> 4) & 0x0f0fu) | ((b1 >> 2) & 0x3030u);
+    *sc = h >= 2 ? sc_hi : sc_lo;
+    *m = h >= 2 ? m_hi : m_lo;
+}
+
+// Q4_K and Q5_K for the split-product verify tile: lane (row, quarter h)
+// turns groups 2h and 2h+1 into the exact f16 integers q * sc (at most
+// 31 * 63 = 1953), returns the block scale d, applied to the F32 block sum,
+// and -dmin * m of its two groups, the F32 weights of the minimum term. The
+// decoded value d * sc * q - dmin * m (quant/decode.zig:163-170, 240-250) is
+// thereby split into two sums that each round nothing but the activations.
+template <uint32_t ENC>
+struct VSplit;
+
+template <>
+struct VSplit<12> {
+    static constexpr uint32_t BLOCK_BYTES = 144, BLOCK_VALUES = 256;
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return VLane<12>::col(h, c); }
+    // 16-byte reads of lane quarter h: NH header reads at 16 j, then two code
+    // reads at CODE + 32 h and CODE + 32 h + 16
+    static constexpr uint32_t NH = 1, CODE = 16;
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&b)[8], float &d,
+                                                   float &nm0, float &nm1) {
+        const uint4 hdr[NH] = {*(const uint4 *)blk};
+        decode<false>(hdr, *(const uint4 *)(blk + CODE + 32 * h), *(const uint4 *)(blk + CODE + 16 + 32 * h), h, b, d,
+                      nm0, nm1);
+    }
+    // PAIR: the branch-free scale unpack (the streamed tile); the register
+    // tile measured faster with the per-group form
+    template <bool PAIR>
+    __device__ __forceinline__ static void decode(const uint4 (&hr)[NH], uint4 q0, uint4 q1, uint32_t h,
+                                                  half8 (&b)[8], float &d, float &nm0, float &nm1) {
+        const uint4 hdr = hr[0];
+        d = half_bits(hdr.x & 0xffffu);
+        const float dmin = half_bits(hdr.x >> 16);
+        uint32_t scp, mp;
+        if constexpr (PAIR) {
+            q4k_scale_min_pair(h, hdr.y, hdr.z, hdr.w, &scp, &mp);
+        } else {
+            uint32_t a0, n0, a1, n1;
+            q4k_scale_min(2 * h, hdr.y, hdr.z, hdr.w, &a0, &n0);
+            q4k_scale_min(2 * h + 1, hdr.y, hdr.z, hdr.w, &a1, &n1);
+            scp = a0 | (a1 << 8);
+            mp = n0 | (n1 << 8);
+        }
+        const uint32_t sc0 = scp & 0xffu, sc1 = scp >> 8;
+        nm0 = -dmin * (float)(mp & 0xffu);
+        nm1 = -dmin * (float)(mp >> 8);
+        // low nibbles at 1024 + q (scale sc), high nibbles at 1024 + 16 q (scale sc / 16)
+        const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)((float)sc1 * 0.0625f);
+        const half2v S0 = {s0, s0}, C0 = {(_Float16)(-1024.f * (float)sc0), (_Float16)(-1024.f * (float)sc0)};
+        const half2v S1 = {s1, s1}, C1 = {(_Float16)(-64.f * (float)sc1), (_Float16)(-64.f * (float)sc1)};
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {  // chunk c: group 2h, c + 4: group 2h + 1 (VLane<12> order)
+            u32x4 lo, hi;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t l4 = w[2 * c + k] & 0x0f0f0f0fu, u4 = w[2 * c + k] & 0xf0f0f0f0u;
+                lo[2 * k] = scaled_codes(f16_biased<0, 1>(l4), S0, C0);
+                lo[2 * k + 1] = scaled_codes(f16_biased<2, 3>(l4), S0, C0);
+                hi[2 * k] = scaled_codes(f16_biased<0, 1>(u4), S1, C1);
+                hi[2 * k + 1] = scaled_codes(f16_biased<2, 3>(u4), S1, C1);
+            }
+            b[c] = __builtin_bit_cast(half8, lo);
+            b[c + 4] = __builtin_bit_cast(half8, hi);
+        }
+    }
+};
+
+template <>
+struct VSplit<13> {
+    static constexpr uint32_t BLOCK_BYTES = 176, BLOCK_VALUES = 256;
+    __device__ __forceinline__ static uint32_t col(uint32_t h, uint32_t c) { return VLane<13>::col(h, c); }
+    static constexpr uint32_t NH = 3, CODE = 48;  // header + qh, codes (as VSplit<12>)
+    __device__ __forceinline__ static void dequant(const uint8_t *blk, uint32_t h, half8 (&b)[8], float &d,
+                                                   float &nm0, float &nm1) {
+        const uint4 hdr[NH] = {*(const uint4 *)blk, *(const uint4 *)(blk + 16), *(const uint4 *)(blk + 32)};
+        decode<false>(hdr, *(const uint4 *)(blk + CODE + 32 * h), *(const uint4 *)(blk + CODE + 16 + 32 * h), h, b, d,
+                      nm0, nm1);
+    }
+    // PAIR: the branch-free scale unpack (the streamed tile); the register
+    // tile measured faster with the per-group form
+    template <bool PAIR>
+    __device__ __forceinline__ static void decode(const uint4 (&hr)[NH], uint4 q0, uint4 q1, uint32_t h,
+                                                  half8 (&b)[8], float &d, float &nm0, float &nm1) {
+        const uint4 hdr = hr[0], h0 = hr[1], h1 = hr[2];
+        d = half_bits(hdr.x & 0xffffu);
+        const float dmin = half_bits(hdr.x >> 16);
+        uint32_t scp, mp;
+        if constexpr (PAIR) {
+            q4k_scale_min_pair(h, hdr.y, hdr.z, hdr.w, &scp, &mp);
+        } else {
+            uint32_t a0, n0, a1, n1;
+            q4k_scale_min(2 * h, hdr.y, hdr.z, hdr.w, &a0, &n0);
+            q4k_scale_min(2 * h + 1, hdr.y, hdr.z, hdr.w, &a1, &n1);
+            scp = a0 | (a1 << 8);
+            mp = n0 | (n1 << 8);
+        }
+        const uint32_t sc0 = scp & 0xffu, sc1 = scp >> 8;
+        nm0 = -dmin * (float)(mp & 0xffu);
+        nm1 = -dmin * (float)(mp >> 8);
+        const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)(float)sc1;
+        const half2v S0 = {s0, s0}, C0 = {(_Float16)(-1024.f * (float)sc0), (_Float16)(-1024.f * (float)sc0)};
+        const half2v S1 = {s1, s1}, C1 = {(_Float16)(-1024.f * (float)sc1), (_Float16)(-1024.f * (float)sc1)};
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            u32x4 lo, hi;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t wd = w[2 * c + k], hd = hb[2 * c + k];
+                const uint32_t l5 = (wd & 0x0f0f0f0fu) | (((hd >> (2 * h)) & 0x01010101u) << 4);
+                const uint32_t u5 = ((wd >> 4) & 0x0f0f0f0fu) | (((hd >> (2 * h + 1)) & 0x01010101u) << 4);
+                lo[2 * k] = scaled_codes(f16_biased<0, 1>(l5), S0, C0);
+                lo[2 * k + 1] = scaled_codes(f16_biased<2, 3>(l5), S0, C0);
+                hi[2 * k] = scaled_codes(f16_biased<0, 1>(u5), S1, C1);
+                hi[2 * k + 1] = scaled_codes(f16_biased<2, 3>(u5), S1, C1);
+            }
+            b[c] = __builtin_bit_cast(half8, lo);
+            b[c + 4] = __builtin_bit_cast(half8, hi);
+        }
+    }
+};
+
 constexpr int VF_MAX_WAVES = 16;
 
 // RG row groups of 16 per wave: the x fragments of a block are loaded once
@@ -1041,17 +1196,458 @@ __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_kernel(const uint8_t
     }
 }
 
+// The split-product verify tile (Q4_K, Q5_K). The activations are the A
+// operand (16 tokens x 32 k) and the weights the B operand, so lane
+// (row r16, quarter h) holds D for its own row and tokens 4h..4h+3 and
+// applies its own block scale d. Per block: eight f16 MFMAs of x against
+// q * sc into a zeroed block sum, one F32 FMA by d, and two F32 MFMAs
+// (16x16x4) of the group sums of x against -dmin * m.
+template <uint32_t ENC, typename XT, int RG>
+__global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_split_kernel(const uint8_t *__restrict__ w,
+                                                                          uint64_t stride, uint32_t rows,
+                                                                          uint32_t nblocks,
+                                                                          const XT *__restrict__ x,
+                                                                          uint64_t in_stride, float *__restrict__ y,
+                                                                          uint64_t out_stride, uint32_t tokens) {
+    __shared__ float part_sums[VF_MAX_WAVES][RG][16][16];
+    using L = VSplit<ENC>;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t r16 = lane & 15, h = lane >> 4;
+    const uint32_t row0 = blockIdx.x * 16 * RG;
+    const bool tok_ok = r16 < tokens;
+    const XT *xrow = x + (uint64_t)(tok_ok ? r16 : 0) * in_stride;
+    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    floatx4 acc[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) acc[g] = zero;
+    for (uint32_t b = wv; b < nblocks; b += nwaves) {
+        half8 bx[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t col = b * L::BLOCK_VALUES + L::col(h, c);
+            // A rows past `tokens` (lanes reading token 0) only reach D rows
+            // that are never stored, so the loads need no guard.
+            if constexpr (sizeof(XT) == 2) {
+                bx[c] = *(const half8 *)((const _Float16 *)xrow + col);
+            } else {
+                const float4 f0 = *(const float4 *)((const float *)xrow + col);
+                const float4 f1 = *(const float4 *)((const float *)xrow + col + 4);
+                bx[c][0] = (_Float16)f0.x; bx[c][1] = (_Float16)f0.y; bx[c][2] = (_Float16)f0.z; bx[c][3] = (_Float16)f0.w;
+                bx[c][4] = (_Float16)f1.x; bx[c][5] = (_Float16)f1.y; bx[c][6] = (_Float16)f1.z; bx[c][7] = (_Float16)f1.w;
+            }
+        }
+        // F32 sums of the (f16) activations of groups 2h and 2h+1, token r16
+        float sx0 = 0.f, sx1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sx0 = __builtin_amdgcn_fdot2(half2v{bx[c][2 * e], bx[c][2 * e + 1]}, ones, sx0, false);
+                sx1 = __builtin_amdgcn_fdot2(half2v{bx[c + 4][2 * e], bx[c + 4][2 * e + 1]}, ones, sx1, false);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            const uint8_t *wrow = w + (uint64_t)min(row0 + 16 * g + r16, rows - 1) * stride;
+            half8 bq[8];
+            float d, nm0, nm1;
+            L::dequant(wrow + (uint64_t)b * L::BLOCK_BYTES, h, bq, d, nm0, nm1);
+            floatx4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[0], bq[0], zero, 0, 0, 0);
+#pragma unroll
+            for (int c = 1; c < 8; ++c) part = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[c], bq[c], part, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(d, part[i], acc[g][i]);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx0, nm0, acc[g], 0, 0, 0);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx1, nm1, acc[g], 0, 0, 0);
+        }
+    }
+    // D layout: lane l holds weight row l%16, tokens 4*(l/16) + i
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part_sums[wv][g][r16][4 * h + i] = acc[g][i];
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < 256 * RG; idx += blockDim.x) {
+        const uint32_t g = idx >> 8, rr = (idx >> 4) & 15, t = idx & 15;
+        float v = 0.f;
+        for (uint32_t k = 0; k < nwaves; ++k) v += part_sums[k][g][rr][t];
+        const uint32_t row = row0 + 16 * g + rr;
+        if (t < tokens && row < rows) y[(uint64_t)t * out_stride + row] = v;
+    }
+}
+
+// The streamed verify tile (Q4_K, Q5_K; K up to 24 blocks). Weights go
+// global -> LDS with global_load_lds_dwordx4 into a two-slot ring per wave,
+// as contiguous whole-row spans, instead of every lane loading its own
+// scattered 16-byte pieces. Each wave owns a fixed run of at most NB blocks
+// of every row: its x fragments and group sums stay in registers for the
+// whole launch. A step is 16 rows x NB blocks. Per-wave partial sums of
+// each (row, token) go to LDS and are added in wave order at the end, so
+// results are the same run to run; the arithmetic is that of
+// verify_split_kernel.
+//
+// LDS: every wave's slot 0, then every wave's slot 1, then the partial sums
+// [row][wave][token]. With f16 activations that fit (STAGE), each wave
+// first copies the activations of its own blocks, contiguous per token,
+// into the slot-1 / partial-sum area and reads its fragments from there: a
+// lane's fragments are 16-byte pieces of 16 token rows, which as direct
+// loads cost one cache line each. The step-1 copies follow a barrier.
+constexpr uint32_t VD_DEPTH = 2;     // ring slots per wave
+constexpr uint32_t VD_MAX_WAVES = 8;  // 256 registers per lane
+
+typedef __attribute__((address_space(3))) uint8_t vd_lds_u8_t;
+__device__ __forceinline__ uint32_t vd_lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(const vd_lds_u8_t *)p; }
+
+template <uint32_t ENC, uint32_t NB>
+struct VDma {
+    using L = VSplit<ENC>;
+    static constexpr uint32_t BYTES = L::BLOCK_BYTES, ROW_BYTES = NB * BYTES;
+    static constexpr uint32_t STEP_CHUNKS = 16 * ROW_BYTES / 16, INSTRS = (STEP_CHUNKS + 63) / 64;
+    static constexpr uint32_t SLOT = STEP_CHUNKS * 16;  // the last copy runs on the lanes it needs
+};
+
+// Ring reads of block S of a step for one lane (row r16, quarter h): the
+// header reads at a + S * BYTES + 16 j, the code reads at c + S * BYTES and
+// + 16, where c = a + CODE + 32 h. No wait: vd_ring_wait follows.
+template <uint32_t ENC, uint32_t S>
+__device__ __forceinline__ void vd_read_block(uint32_t a, uint32_t c, u32x4 (&r)[VSplit<ENC>::NH], u32x4 (&q)[2]) {
+    constexpr uint32_t O = S * VSplit<ENC>::BLOCK_BYTES;
+    if constexpr (VSplit<ENC>::NH == 1) {
+        asm volatile(
+            "ds_read_b128 %0, %3 offset:%5\n\t"
+            "ds_read_b128 %1, %4 offset:%5\n\t"
+            "ds_read_b128 %2, %4 offset:%6"
+            : "=&v"(r[0]), "=&v"(q[0]), "=&v"(q[1])
+            : "v"(a), "v"(c), "n"(O), "n"(O + 16)
+            : "memory");
+    } else {
+        static_assert(VSplit<ENC>::NH == 3, "header reads");
+        asm volatile(
+            "ds_read_b128 %0, %5 offset:%7\n\t"
+            "ds_read_b128 %1, %5 offset:%8\n\t"
+            "ds_read_b128 %2, %5 offset:%9\n\t"
+            "ds_read_b128 %3, %6 offset:%7\n\t"
+            "ds_read_b128 %4, %6 offset:%8"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(q[0]), "=&v"(q[1])
+            : "v"(a), "v"(c), "n"(O), "n"(O + 16), "n"(O + 32)
+            : "memory");
+    }
+}
+
+template <uint32_t ENC, uint32_t NB, int VM>
+__device__ __forceinline__ void vd_ring_read(uint32_t a, uint32_t c, uint4 (&hd)[NB][VSplit<ENC>::NH],
+                                             uint4 (&cq)[NB][2]) {
+    constexpr uint32_t NH = VSplit<ENC>::NH;
+    u32x4 r[NB][NH], q[NB][2];
+    // the ring slot's copies are older than the VM copies of younger steps
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(VM) : "memory");
+    vd_read_block<ENC, 0>(a, c, r[0], q[0]);
+    vd_read_block<ENC, 1>(a, c, r[1], q[1]);
+    if constexpr (NB > 2) vd_read_block<ENC, 2>(a, c, r[2], q[2]);
+    static_assert(NB == 2 || NB == 3, "blocks per wave");
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    // the registers are defined after the wait, as far as the compiler knows
+#pragma unroll
+    for (uint32_t s = 0; s < NB; ++s) {
+#pragma unroll
+        for (uint32_t j = 0; j < NH; ++j) {
+            asm volatile("" : "+v"(r[s][j]));
+            hd[s][j] = make_uint4(r[s][j].x, r[s][j].y, r[s][j].z, r[s][j].w);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            asm volatile("" : "+v"(q[s][j]));
+            cq[s][j] = make_uint4(q[s][j].x, q[s][j].y, q[s][j].z, q[s][j].w);
+        }
+    }
+}
+
+// Fragment reads of one block of staged activations: the lane's 128
+// contiguous bytes at a + O (chunks c = 0..7 at 16 c). No wait.
+template <uint32_t O>
+__device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
+    asm volatile(
+        "ds_read_b128 %0, %8 offset:%9\n\t"
+        "ds_read_b128 %1, %8 offset:%10\n\t"
+        "ds_read_b128 %2, %8 offset:%11\n\t"
+        "ds_read_b128 %3, %8 offset:%12\n\t"
+        "ds_read_b128 %4, %8 offset:%13\n\t"
+        "ds_read_b128 %5, %8 offset:%14\n\t"
+        "ds_read_b128 %6, %8 offset:%15\n\t"
+        "ds_read_b128 %7, %8 offset:%16"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(a), "n"(O), "n"(O + 16), "n"(O + 32), "n"(O + 48), "n"(O + 64), "n"(O + 80), "n"(O + 96),
+          "n"(O + 112)
+        : "memory");
+}
+
+template <uint32_t ENC, uint32_t NB, typename XT, bool STAGE>
+__global__ void __launch_bounds__(64 * VD_MAX_WAVES) verify_dma_kernel(const uint8_t *__restrict__ w,
+                                                                        uint64_t stride, uint32_t rows,
+                                                                        uint32_t nblocks, const XT *__restrict__ x,
+                                                                        uint64_t in_stride, float *__restrict__ y,
+                                                                        uint64_t out_stride, uint32_t tokens,
+                                                                        uint32_t tpad) {
+    using L = VSplit<ENC>;
+    using V = VDma<ENC, NB>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t vd_lds[];
+    const uint32_t lane = threadIdx.x & 63, kw = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t r16 = lane & 15, h = lane >> 4;
+    uint8_t *ring = vd_lds + kw * V::SLOT;  // slot d at + d * nwaves * SLOT
+    const uint32_t slot_stride = nwaves * V::SLOT;
+    float *partial = (float *)(vd_lds + VD_DEPTH * slot_stride);  // [row][wave][tpad]
+    // balanced row ranges: every workgroup holds at least 16 rows (the host
+    // launches at most rows / 16 workgroups)
+    const uint32_t row_begin = (uint32_t)((uint64_t)blockIdx.x * rows / gridDim.x);
+    const uint32_t nrow = (uint32_t)((uint64_t)(blockIdx.x + 1) * rows / gridDim.x) - row_begin;
+    const uint32_t nsteps = (nrow + 15) / 16;
+    // Wave kw runs on SIMD kw % 4 next to wave kw + 4, so the runs are cut
+    // in the order (kw % 4, kw / 4): each SIMD's two waves hold about
+    // nblocks / 4 blocks between them (20 blocks: 3 + 2 on every SIMD).
+    const uint32_t pos = nwaves == 8 ? (kw & 3) * 2 + (kw >> 2) : kw;
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane(pos * nblocks / nwaves);
+    const uint32_t nlive = __builtin_amdgcn_readfirstlane((pos + 1) * nblocks / nwaves - b0);  // 1 .. NB
+
+    // This lane's chunk of each copy: row q of the step and byte offset in
+    // the row (chunks past the step repeat the last one; a block past the
+    // row's end copies the wave's first block again, so every copy stays in
+    // the row).
+    // A step's 16 rows start at row min(16 i, nrow - 16) of the range: the
+    // last step moves back to end at the range's last row, and stores only
+    // the rows no earlier step stored. So every copy is a uniform step base
+    // plus this lane's fixed 32-bit offset (16 rows span < 4 GiB).
+    uint32_t doff[V::INSTRS];
+#pragma unroll
+    for (uint32_t n = 0; n < V::INSTRS; ++n) {
+        const uint32_t k = min(64 * n + lane, V::STEP_CHUNKS - 1);
+        const uint32_t in_row = 16 * (k % (V::ROW_BYTES / 16)), sblk = in_row / V::BYTES;
+        doff[n] = (k / (V::ROW_BYTES / 16)) * (uint32_t)stride + b0 * V::BYTES +
+                  (sblk < nlive ? in_row : in_row - sblk * V::BYTES);
+    }
+    const uint8_t *wg_base = w + (uint64_t)row_begin * stride;
+#define NUQ_VD_DMA(SLOT_, STEP_)                                                                          \
+    {                                                                                                   \
+        const uint8_t *sbase_ = wg_base + (uint64_t)min(16 * (STEP_), nrow - 16) * stride;              \
+        _Pragma("unroll") for (uint32_t n = 0; n < V::INSTRS; ++n) {                                    \
+            if (64 * (n + 1) <= V::STEP_CHUNKS || 64 * n + lane < V::STEP_CHUNKS)                          \
+                __builtin_amdgcn_global_load_lds((global_void_t *)(sbase_ + doff[n]),                     \
+                                                 (lds_void_t *)(ring + (SLOT_) * slot_stride + n * 1024), 16, 0, 2); \
+        }                                                                                               \
+    }
+    half8 bx[NB][8];
+    if constexpr (STAGE) {
+        // this wave's activations, [token][its blocks' 512 bytes], copied
+        // before the step-0 weights so that they are waited for alone
+        const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
+        const uint32_t xs = (uint32_t)(nwaves * V::SLOT + b0 * tokens * 512);
+        for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
+            const uint32_t k = 64 * jx + lane;
+            if (k < xchunks) {
+                const uint32_t t = k / (span / 16), rem = k - t * (span / 16);
+                const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
+                __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(vd_lds + xs + 1024 * jx), 16,
+                                                 0, 0);
+            }
+        }
+        NUQ_VD_DMA(0, 0)
+        asm volatile("s_waitcnt vmcnt(%0)" : : "n"(V::INSTRS) : "memory");
+        // lanes of tokens past `tokens` read token 0: they reach only D rows
+        // that are never stored
+        const uint32_t xa = vd_lds_addr(vd_lds) + xs + (r16 < tokens ? r16 : 0) * span + 128 * h;
+        u32x4 xr[NB][8] = {};  // a wave's block past the row's end stays zero
+        vd_read_x<0>(xa, xr[0]);
+        if (nlive > 1) vd_read_x<512>(xa, xr[1]);
+        if constexpr (NB > 2) {
+            if (nlive > 2) vd_read_x<1024>(xa, xr[2]);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+#pragma unroll
+        for (uint32_t s = 0; s < NB; ++s)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                asm volatile("" : "+v"(xr[s][c]));
+                bx[s][c] = __builtin_bit_cast(half8, xr[s][c]);
+            }
+        // every wave has its fragments: the staging area becomes slot 1
+        __builtin_amdgcn_s_barrier();
+        if (nsteps > 1) NUQ_VD_DMA(1, 1)
+    } else {
+#pragma unroll
+        for (uint32_t d = 0; d < VD_DEPTH; ++d)
+            if (d < nsteps) NUQ_VD_DMA(d, d)
+
+        // x fragments of the wave's blocks, loaded after the first copies are
+        // on their way. A rows past `tokens` are zero; they reach only D rows
+        // that are never stored.
+        const bool tok_ok = r16 < tokens;
+        const XT *xrow = x + (uint64_t)(tok_ok ? r16 : 0) * in_stride;
+#pragma unroll
+        for (uint32_t s = 0; s < NB; ++s) {
+            const uint32_t blk = s < nlive ? b0 + s : b0;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t col = blk * L::BLOCK_VALUES + L::col(h, c);
+                bx[s][c] = half8{};
+                if (tok_ok) {
+                    if constexpr (sizeof(XT) == 2) {
+                        bx[s][c] = *(const half8 *)((const _Float16 *)xrow + col);
+                    } else {
+                        const float4 f0 = *(const float4 *)((const float *)xrow + col);
+                        const float4 f1 = *(const float4 *)((const float *)xrow + col + 4);
+                        bx[s][c] = half8{(_Float16)f0.x, (_Float16)f0.y, (_Float16)f0.z, (_Float16)f0.w,
+                                         (_Float16)f1.x, (_Float16)f1.y, (_Float16)f1.z, (_Float16)f1.w};
+                    }
+                }
+            }
+        }
+    }
+
+    // F32 sums of the f16 activations of groups 2h and 2h+1 of each block
+    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+    float sx[NB][2];
+#pragma unroll
+    for (uint32_t s = 0; s < NB; ++s) {
+        sx[s][0] = sx[s][1] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sx[s][0] = __builtin_amdgcn_fdot2(half2v{bx[s][c][2 * e], bx[s][c][2 * e + 1]}, ones, sx[s][0], false);
+                sx[s][1] = __builtin_amdgcn_fdot2(half2v{bx[s][c + 4][2 * e], bx[s][c + 4][2 * e + 1]}, ones,
+                                                  sx[s][1], false);
+            }
+    }
+
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t ring_a = vd_lds_addr(ring) + r16 * V::ROW_BYTES;
+    const uint32_t part_a = vd_lds_addr((const uint8_t *)partial) + ((r16 * nwaves + kw) * tpad + 4 * h) * 4;
+    const uint32_t part_step = 16 * nwaves * tpad * 4;
+    const bool store_tokens = 4 * h < tpad;
+    for (uint32_t i = 0; i < nsteps; ++i) {
+        const uint32_t slot = i & (VD_DEPTH - 1);
+        uint4 hd[NB][L::NH], cq[NB][2];
+        const uint32_t a = ring_a + slot * slot_stride;
+        // the next step's copies may still be in flight, except on the last
+        if (i + 1 < nsteps)
+            vd_ring_read<ENC, NB, V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
+        else
+            vd_ring_read<ENC, NB, 0>(a, a + L::CODE + 32 * h, hd, cq);
+        if (i + VD_DEPTH < nsteps) NUQ_VD_DMA(slot, i + VD_DEPTH)
+        // independent MFMA chains: one per block, one for the minimum terms
+        floatx4 part[NB], accm = zero;
+        float d[NB];
+#pragma unroll
+        for (uint32_t s = 0; s < NB; ++s) {
+            if (s >= nlive) break;
+            half8 bq[8];
+            float nm0, nm1;
+            L::template decode<true>(hd[s], cq[s][0], cq[s][1], h, bq, d[s], nm0, nm1);
+            part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][0], bq[0], zero, 0, 0, 0);
+#pragma unroll
+            for (int c = 1; c < 8; ++c)
+                part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][c], bq[c], part[s], 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][0], nm0, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][1], nm1, accm, 0, 0, 0);
+        }
+        floatx4 acc = accm;
+#pragma unroll
+        for (uint32_t s = 0; s < NB; ++s) {
+            if (s >= nlive) break;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(d[s], part[s][e], acc[e]);
+        }
+        // D: lane holds row base + r16 (base = min(16 i, nrow - 16)), tokens
+        // 4h..4h+3; rows an earlier step stored are skipped (written through
+        // asm: the compiler would otherwise wait for every ring copy in flight)
+        const uint32_t base = min(16 * i, nrow - 16);
+        if (store_tokens && base + r16 >= 16 * i)
+            asm volatile("ds_write_b128 %0, %1" : : "v"(part_a + base * (part_step / 16)), "v"(acc) : "memory");
+    }
+#undef NUQ_VD_DMA
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < nrow * tokens; idx += blockDim.x) {
+        const uint32_t t = idx / nrow, r = idx - t * nrow;
+        float v = 0.f;
+        for (uint32_t k = 0; k < nwaves; ++k) v += partial[(r * nwaves + k) * tpad + t];
+        y[(uint64_t)t * out_stride + row_begin + r] = v;
+    }
+}
+
+template <uint32_t ENC, uint32_t NB>
+static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
+                                       uint32_t nblocks, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
+                                       uint64_t out_stride, uint32_t tokens, uint32_t tpad, uint32_t wgs,
+                                       size_t lds, bool stage) {
+    const dim3 grid(wgs), block(64 * std::min(nblocks, VD_MAX_WAVES));
+    if (x_f16 && stage)
+        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, true>), grid, block, lds, s, w, stride, rows,
+                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad);
+    else if (x_f16)
+        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, false>), grid, block, lds, s, w, stride, rows,
+                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad);
+    else
+        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, float, false>), grid, block, lds, s, w, stride, rows,
+                           nblocks, (const float *)x, in_stride, y, out_stride, tokens, tpad);
+    return hipGetLastError();
+}
+
+// Streams when the row's blocks fit 8 waves of at most 3 blocks; returns
+// false (nothing launched) otherwise.
+template <uint32_t ENC>
+static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
+                              const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
+                              uint32_t tokens, hipError_t *err) {
+    if (rows < 16 || nblocks > 3 * VD_MAX_WAVES) return false;
+    const uint32_t nb = nblocks > 2 * VD_MAX_WAVES ? 3 : 2;
+    const uint32_t waves = std::min(nblocks, VD_MAX_WAVES);  // runs of at most nb blocks
+    const uint32_t tpad = (tokens + 3) & ~3u;
+    const size_t slot = nb == 3 ? VDma<ENC, 3>::SLOT : VDma<ENC, 2>::SLOT;
+    const size_t rings = (size_t)waves * VD_DEPTH * slot, per_row = (size_t)waves * tpad * 4;
+    if (rings + 16 * per_row > 160 * 1024) return false;
+    // One workgroup per CU while the partial sums fit, else more, shorter
+    // row ranges; never more than rows / 16 workgroups, so each range holds
+    // at least 16 rows (the kernel's steps assume it). Ranges differ by at
+    // most one row.
+    const uint32_t max_rows = (uint32_t)((160 * 1024 - rings) / per_row);
+    uint32_t wgs = std::max(256u, (rows + max_rows - 1) / max_rows);
+    wgs = std::min(wgs, rows / 16);
+    const uint32_t rows_per_wg = (rows + wgs - 1) / wgs;  // the longest range
+    if (rows_per_wg > max_rows) return false;
+    // staged activations: [token][K] f16 after the slot-0 area
+    const size_t staged = (size_t)waves * slot + (size_t)tokens * nblocks * 512;
+    // (16-byte copies: the entry points accept only 16-byte aligned rows)
+    const bool stage = x_f16 && staged <= 160 * 1024;
+    const size_t lds = std::max(rings + rows_per_wg * per_row, stage ? staged : 0);
+    *err = nb == 3 ? launch_verify_dma_nb<ENC, 3>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride,
+                                                  tokens, tpad, wgs, lds, stage)
+                   : launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride,
+                                                  tokens, tpad, wgs, lds, stage);
+    return true;
+}
+
 template <uint32_t ENC, int RG>
 static hipError_t launch_verify_rg(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                                    uint32_t waves, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                    uint64_t out_stride, uint32_t tokens) {
     dim3 grid((rows + 16 * RG - 1) / (16 * RG)), block(64 * waves);
-    if (x_f16)
-        hipLaunchKernelGGL((verify_kernel<ENC, _Float16, RG>), grid, block, 0, s, w, stride, rows, nblocks,
-                           (const _Float16 *)x, in_stride, y, out_stride, tokens);
-    else
-        hipLaunchKernelGGL((verify_kernel<ENC, float, RG>), grid, block, 0, s, w, stride, rows, nblocks,
-                           (const float *)x, in_stride, y, out_stride, tokens);
+    if constexpr (ENC == 12 || ENC == 13) {
+        if (x_f16)
+            hipLaunchKernelGGL((verify_split_kernel<ENC, _Float16, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                               (const _Float16 *)x, in_stride, y, out_stride, tokens);
+        else
+            hipLaunchKernelGGL((verify_split_kernel<ENC, float, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                               (const float *)x, in_stride, y, out_stride, tokens);
+    } else {
+        if (x_f16)
+            hipLaunchKernelGGL((verify_kernel<ENC, _Float16, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                               (const _Float16 *)x, in_stride, y, out_stride, tokens);
+        else
+            hipLaunchKernelGGL((verify_kernel<ENC, float, RG>), grid, block, 0, s, w, stride, rows, nblocks,
+                               (const float *)x, in_stride, y, out_stride, tokens);
+    }
     return hipGetLastError();
 }
 
@@ -1060,6 +1656,11 @@ static hipError_t launch_verify_enc(hipStream_t s, const uint8_t *w, uint64_t st
                                     uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                     uint64_t out_stride, uint32_t tokens) {
     const uint32_t nblocks = columns / 256;
+    if constexpr (ENC == 12 || ENC == 13) {
+        hipError_t err;
+        if (launch_verify_dma<ENC>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, &err))
+            return err;
+    }
     // About five blocks per wave (at most VF_MAX_WAVES waves), split evenly:
     // measured best at K = 5120 (4 waves) and K = 17408 (14 waves).
     const uint32_t per_wave = std::max(5u, (nblocks + VF_MAX_WAVES - 1) / VF_MAX_WAVES);

@@ -271,7 +271,56 @@ def test_tile_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
     check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, "tile")
 
 
-@pytest.mark.parametrize("encoding,rows,columns,tokens", [(12, 5120, 17408, 512), (14, 2048, 5120, 1024)])
+# The streamed verify tile (Q4_K and Q5_K, tokens <= 16, up to 24 blocks per
+# row): 2 and 3 blocks per wave, a wave whose last block is past the row
+# (odd block counts), 16-row steps that end mid-step, token counts 1..16,
+# and row ranges shortened so the partial sums fit the LDS (13, 12000, 6144,
+# 16). The weights enter the MFMAs as exact f16 integers q * sc, so only the
+# activations are rounded.
+VERIFY_DMA_CASES = [(12, 17408, 5120, 8), (12, 4104, 5120, 8), (13, 1000, 4608, 16), (12, 2000, 6144, 3),
+                    (12, 808, 3840, 13), (13, 12000, 6144, 16), (12, 24, 256, 1), (13, 4104, 5120, 8)]
+
+
+@pytest.mark.parametrize("xdtype", ["f16", "f32"])
+@pytest.mark.parametrize("encoding,rows,columns,tokens", VERIFY_DMA_CASES)
+def test_streamed_verify_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
+    import torch
+    w = quantized(encoding, rows, columns, 40 + tokens)
+    x32 = gaussian(50 + tokens, (tokens, columns))
+    xref = x32.astype(np.float16).astype(np.float32) if xdtype == "f16" else x32
+    xg = to_gpu(x32.astype(np.float16)) if xdtype == "f16" else to_gpu(x32)
+    out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+    print(f"[verify] enc {encoding} {rows}x{columns} tokens {tokens} {xdtype}", flush=True)
+    backend.matmul_kernel(nq.KERNEL_TILE, nq.Matrix(encoding, rows, columns, to_gpu(w)), xg, columns, out, rows, tokens)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, xref)
+    k = F16_K / 2 if xdtype == "f16" else F16_K
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, "verify")
+
+
+@pytest.mark.parametrize("pad", [8, 64])
+def test_streamed_verify_strided_activations(backend, pad):
+    """f16 activation rows `pad` halves longer than K (staged through LDS in
+    16-byte pieces) match the oracle; rows that are not 16-byte aligned are
+    refused before any launch."""
+    import torch
+    encoding, rows, columns, tokens = 12, 808, 5120, 8
+    w = quantized(encoding, rows, columns, 61)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    x = np.zeros((tokens, columns + pad), np.float16)
+    x[:, :columns] = gaussian(62, (tokens, columns)).astype(np.float16)
+    out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_TILE, m, to_gpu(x), columns + pad, out, rows, tokens)
+    backend.sync()
+    xref = x[:, :columns].astype(np.float32)
+    want = orc.matmul(encoding, rows, columns, w, xref)
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), F16_K / 2, f"pad {pad}")
+    odd = to_gpu(np.zeros((tokens, columns + 4), np.float16))
+    with pytest.raises(nq.InvalidShape):
+        backend.matmul_kernel(nq.KERNEL_TILE, m, odd, columns + 4, out, rows, tokens)
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens", [(12, 5120, 17408, 512), (14, 2048, 5120, 1024), (12, 17408, 5120, 8)])
 def test_prefill_split_k_is_deterministic(backend, encoding, rows, columns, tokens):
     """Tiles split along K are summed in split order by whichever split
     finishes last: repeated launches must agree bit for bit."""
