@@ -1288,14 +1288,18 @@ __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_split_kernel(const u
 // results are the same run to run; the arithmetic is that of
 // verify_split_kernel.
 //
-// LDS: every wave's slot 0, then every wave's slot 1, then the partial sums
-// [row][wave][token]. With f16 activations that fit (STAGE), each wave
-// first copies the activations of its own blocks, contiguous per token,
-// into the slot-1 / partial-sum area and reads its fragments from there: a
-// lane's fragments are 16-byte pieces of 16 token rows, which as direct
-// loads cost one cache line each. The step-1 copies follow a barrier.
+// LDS: one region per wave (its slot 0, its slot 1 and, when staging, the
+// extra bytes its activations need past slot 1), then the partial sums
+// [row][wave][token]. With f16 activations (STAGE) each wave first copies
+// the activations of its own blocks, contiguous per token, into its slot 1
+// and reads its fragments from there: a lane's fragments are 16-byte pieces
+// of 16 token rows, which as direct loads cost one cache line each. No other
+// wave touches the region, so the step-1 copies follow at once.
 constexpr uint32_t VD_DEPTH = 2;     // ring slots per wave
-constexpr uint32_t VD_MAX_WAVES = 8;  // 256 registers per lane
+// waves per workgroup: runs of 2 blocks fit 170 registers (3 waves per
+// SIMD), runs of 3 need 256 (2 per SIMD)
+template <uint32_t NB>
+constexpr uint32_t vd_max_waves() { return NB == 2 ? 12 : 8; }
 
 typedef __attribute__((address_space(3))) uint8_t vd_lds_u8_t;
 __device__ __forceinline__ uint32_t vd_lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(const vd_lds_u8_t *)p; }
@@ -1384,31 +1388,28 @@ __device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
 }
 
 template <uint32_t ENC, uint32_t NB, typename XT, bool STAGE>
-__global__ void __launch_bounds__(64 * VD_MAX_WAVES) verify_dma_kernel(const uint8_t *__restrict__ w,
+__global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w,
                                                                         uint64_t stride, uint32_t rows,
                                                                         uint32_t nblocks, const XT *__restrict__ x,
                                                                         uint64_t in_stride, float *__restrict__ y,
                                                                         uint64_t out_stride, uint32_t tokens,
-                                                                        uint32_t tpad) {
+                                                                        uint32_t tpad, uint32_t region) {
     using L = VSplit<ENC>;
     using V = VDma<ENC, NB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t vd_lds[];
     const uint32_t lane = threadIdx.x & 63, kw = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t r16 = lane & 15, h = lane >> 4;
-    uint8_t *ring = vd_lds + kw * V::SLOT;  // slot d at + d * nwaves * SLOT
-    const uint32_t slot_stride = nwaves * V::SLOT;
-    float *partial = (float *)(vd_lds + VD_DEPTH * slot_stride);  // [row][wave][tpad]
+    uint8_t *ring = vd_lds + __builtin_amdgcn_readfirstlane(kw * region);  // slot d at + d * SLOT
+    constexpr uint32_t slot_stride = V::SLOT;
+    float *partial = (float *)(vd_lds + nwaves * region);  // [row][wave][tpad]
     // balanced row ranges: every workgroup holds at least 16 rows (the host
     // launches at most rows / 16 workgroups)
     const uint32_t row_begin = (uint32_t)((uint64_t)blockIdx.x * rows / gridDim.x);
     const uint32_t nrow = (uint32_t)((uint64_t)(blockIdx.x + 1) * rows / gridDim.x) - row_begin;
     const uint32_t nsteps = (nrow + 15) / 16;
-    // Wave kw runs on SIMD kw % 4 next to wave kw + 4, so the runs are cut
-    // in the order (kw % 4, kw / 4): each SIMD's two waves hold about
-    // nblocks / 4 blocks between them (20 blocks: 3 + 2 on every SIMD).
-    const uint32_t pos = nwaves == 8 ? (kw & 3) * 2 + (kw >> 2) : kw;
-    const uint32_t b0 = __builtin_amdgcn_readfirstlane(pos * nblocks / nwaves);
-    const uint32_t nlive = __builtin_amdgcn_readfirstlane((pos + 1) * nblocks / nwaves - b0);  // 1 .. NB
+    // wave kw owns blocks [kw nblocks / nwaves, (kw + 1) nblocks / nwaves)
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane(kw * nblocks / nwaves);
+    const uint32_t nlive = __builtin_amdgcn_readfirstlane((kw + 1) * nblocks / nwaves - b0);  // 1 .. NB
 
     // This lane's chunk of each copy: row q of the step and byte offset in
     // the row (chunks past the step repeat the last one; a block past the
@@ -1438,24 +1439,24 @@ __global__ void __launch_bounds__(64 * VD_MAX_WAVES) verify_dma_kernel(const uin
     }
     half8 bx[NB][8];
     if constexpr (STAGE) {
-        // this wave's activations, [token][its blocks' 512 bytes], copied
-        // before the step-0 weights so that they are waited for alone
+        // this wave's activations, [token][its blocks' 512 bytes], into its
+        // slot 1 (and the extra bytes after it), copied before the step-0
+        // weights so that they are waited for alone
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
-        const uint32_t xs = (uint32_t)(nwaves * V::SLOT + b0 * tokens * 512);
+        uint8_t *xs = ring + V::SLOT;
         for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
             const uint32_t k = 64 * jx + lane;
             if (k < xchunks) {
                 const uint32_t t = k / (span / 16), rem = k - t * (span / 16);
                 const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
-                __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(vd_lds + xs + 1024 * jx), 16,
-                                                 0, 0);
+                __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(xs + 1024 * jx), 16, 0, 0);
             }
         }
         NUQ_VD_DMA(0, 0)
         asm volatile("s_waitcnt vmcnt(%0)" : : "n"(V::INSTRS) : "memory");
         // lanes of tokens past `tokens` read token 0: they reach only D rows
         // that are never stored
-        const uint32_t xa = vd_lds_addr(vd_lds) + xs + (r16 < tokens ? r16 : 0) * span + 128 * h;
+        const uint32_t xa = vd_lds_addr(xs) + (r16 < tokens ? r16 : 0) * span + 128 * h;
         u32x4 xr[NB][8] = {};  // a wave's block past the row's end stays zero
         vd_read_x<0>(xa, xr[0]);
         if (nlive > 1) vd_read_x<512>(xa, xr[1]);
@@ -1470,8 +1471,7 @@ __global__ void __launch_bounds__(64 * VD_MAX_WAVES) verify_dma_kernel(const uin
                 asm volatile("" : "+v"(xr[s][c]));
                 bx[s][c] = __builtin_bit_cast(half8, xr[s][c]);
             }
-        // every wave has its fragments: the staging area becomes slot 1
-        __builtin_amdgcn_s_barrier();
+        // the fragments are in registers: slot 1 takes its first step
         if (nsteps > 1) NUQ_VD_DMA(1, 1)
     } else {
 #pragma unroll
@@ -1580,32 +1580,43 @@ template <uint32_t ENC, uint32_t NB>
 static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
                                        uint32_t nblocks, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                        uint64_t out_stride, uint32_t tokens, uint32_t tpad, uint32_t wgs,
-                                       size_t lds, bool stage) {
-    const dim3 grid(wgs), block(64 * std::min(nblocks, VD_MAX_WAVES));
+                                       size_t lds, bool stage, uint32_t region, uint32_t waves) {
+    const dim3 grid(wgs), block(64 * waves);
     if (x_f16 && stage)
         hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, true>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad);
+                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad, region);
     else if (x_f16)
         hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, false>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad);
+                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad, region);
     else
         hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, float, false>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const float *)x, in_stride, y, out_stride, tokens, tpad);
+                           nblocks, (const float *)x, in_stride, y, out_stride, tokens, tpad, region);
     return hipGetLastError();
 }
 
-// Streams when the row's blocks fit 8 waves of at most 3 blocks; returns
+// Streams when the row's blocks fit 12 waves of 2 blocks; returns
 // false (nothing launched) otherwise.
 template <uint32_t ENC>
 static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                               const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
                               uint32_t tokens, hipError_t *err) {
-    if (rows < 16 || nblocks > 3 * VD_MAX_WAVES) return false;
-    const uint32_t nb = nblocks > 2 * VD_MAX_WAVES ? 3 : 2;
-    const uint32_t waves = std::min(nblocks, VD_MAX_WAVES);  // runs of at most nb blocks
+    if (rows < 16 || nblocks > 2 * vd_max_waves<2>()) return false;
+    // Runs of 2 blocks: equal work per wave and up to 3 waves per SIMD
+    // measured faster than runs of 3 (2 waves per SIMD) at K = 20 blocks.
+    const uint32_t waves = (nblocks + 1) / 2;  // the kernel's LDS layout is sized for exactly this many
     const uint32_t tpad = (tokens + 3) & ~3u;
-    const size_t slot = nb == 3 ? VDma<ENC, 3>::SLOT : VDma<ENC, 2>::SLOT;
-    const size_t rings = (size_t)waves * VD_DEPTH * slot, per_row = (size_t)waves * tpad * 4;
+    const size_t slot = VDma<ENC, 2>::SLOT;
+    const size_t per_row = (size_t)waves * tpad * 4;
+    // Staged f16 activations (16-byte copies: the entry points accept only
+    // 16-byte aligned rows) need tokens x 1024 bytes per wave from slot 1 on.
+    const size_t xbytes = (size_t)tokens * 2 * 512;
+    bool stage = x_f16 != 0;
+    size_t region = 2 * slot + (stage && xbytes > slot ? xbytes - slot : 0);
+    if (stage && (size_t)waves * region + 16 * per_row > 160 * 1024) {
+        stage = false;
+        region = 2 * slot;
+    }
+    const size_t rings = (size_t)waves * region;
     if (rings + 16 * per_row > 160 * 1024) return false;
     // One workgroup per CU while the partial sums fit, else more, shorter
     // row ranges; never more than rows / 16 workgroups, so each range holds
@@ -1616,15 +1627,9 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     wgs = std::min(wgs, rows / 16);
     const uint32_t rows_per_wg = (rows + wgs - 1) / wgs;  // the longest range
     if (rows_per_wg > max_rows) return false;
-    // staged activations: [token][K] f16 after the slot-0 area
-    const size_t staged = (size_t)waves * slot + (size_t)tokens * nblocks * 512;
-    // (16-byte copies: the entry points accept only 16-byte aligned rows)
-    const bool stage = x_f16 && staged <= 160 * 1024;
-    const size_t lds = std::max(rings + rows_per_wg * per_row, stage ? staged : 0);
-    *err = nb == 3 ? launch_verify_dma_nb<ENC, 3>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride,
-                                                  tokens, tpad, wgs, lds, stage)
-                   : launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride,
-                                                  tokens, tpad, wgs, lds, stage);
+    const size_t lds = rings + rows_per_wg * per_row;
+    *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, tpad,
+                                        wgs, lds, stage, (uint32_t)region, waves);
     return true;
 }
 
