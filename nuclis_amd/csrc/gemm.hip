@@ -1288,13 +1288,17 @@ __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_split_kernel(const u
 // results are the same run to run; the arithmetic is that of
 // verify_split_kernel.
 //
-// LDS: one region per wave (its slot 0, its slot 1 and, when staging, the
-// extra bytes its activations need past slot 1), then the partial sums
-// [row][wave][token]. With f16 activations (STAGE) each wave first copies
-// the activations of its own blocks, contiguous per token, into its slot 1
-// and reads its fragments from there: a lane's fragments are 16-byte pieces
-// of 16 token rows, which as direct loads cost one cache line each. No other
-// wave touches the region, so the step-1 copies follow at once.
+// With f16 activations each wave first copies the activations of its own
+// blocks, contiguous per token, into LDS and reads its fragments from
+// there: a lane's fragments are 16-byte pieces of 16 token rows, which as
+// direct loads cost one cache line each. LDS layouts (STAGE):
+//   0, 1: one region per wave (its slot 0, its slot 1 and, for 1, the extra
+//         bytes its activations need past slot 1), then the partial sums
+//         [row][wave][token]. No other wave touches a wave's region, so its
+//         step-1 copies follow its fragment reads at once.
+//   2:    every wave's slot 0, every wave's slot 1, the partial sums; the
+//         activations are staged over the slot-1s and partial sums, so a
+//         barrier separates the fragment reads from the step-1 copies.
 constexpr uint32_t VD_DEPTH = 2;     // ring slots per wave
 // waves per workgroup: runs of 2 blocks fit 170 registers (3 waves per
 // SIMD), runs of 3 need 256 (2 per SIMD)
@@ -1387,21 +1391,22 @@ __device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
         : "memory");
 }
 
-template <uint32_t ENC, uint32_t NB, typename XT, bool STAGE>
+template <uint32_t ENC, uint32_t NB, typename XT, int STAGE>
 __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w,
                                                                         uint64_t stride, uint32_t rows,
                                                                         uint32_t nblocks, const XT *__restrict__ x,
                                                                         uint64_t in_stride, float *__restrict__ y,
                                                                         uint64_t out_stride, uint32_t tokens,
-                                                                        uint32_t tpad, uint32_t region) {
+                                                                        uint32_t tpad, uint32_t region,
+                                                                        uint32_t slot_gap, uint32_t part_off) {
     using L = VSplit<ENC>;
     using V = VDma<ENC, NB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t vd_lds[];
     const uint32_t lane = threadIdx.x & 63, kw = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t r16 = lane & 15, h = lane >> 4;
-    uint8_t *ring = vd_lds + __builtin_amdgcn_readfirstlane(kw * region);  // slot d at + d * SLOT
-    constexpr uint32_t slot_stride = V::SLOT;
-    float *partial = (float *)(vd_lds + nwaves * region);  // [row][wave][tpad]
+    uint8_t *ring = vd_lds + __builtin_amdgcn_readfirstlane(kw * region);  // slot d at + d * slot_gap
+    const uint32_t slot_stride = slot_gap;
+    float *partial = (float *)(vd_lds + part_off);  // [row][wave][tpad]
     // balanced row ranges: every workgroup holds at least 16 rows (the host
     // launches at most rows / 16 workgroups)
     const uint32_t row_begin = (uint32_t)((uint64_t)blockIdx.x * rows / gridDim.x);
@@ -1438,12 +1443,11 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         }                                                                                               \
     }
     half8 bx[NB][8];
-    if constexpr (STAGE) {
-        // this wave's activations, [token][its blocks' 512 bytes], into its
-        // slot 1 (and the extra bytes after it), copied before the step-0
-        // weights so that they are waited for alone
+    if constexpr (STAGE != 0) {
+        // this wave's activations, [token][its blocks' 512 bytes], copied
+        // before the step-0 weights so that they are waited for alone
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
-        uint8_t *xs = ring + V::SLOT;
+        uint8_t *xs = STAGE == 1 ? ring + V::SLOT : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
         for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
             const uint32_t k = 64 * jx + lane;
             if (k < xchunks) {
@@ -1472,6 +1476,7 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
                 bx[s][c] = __builtin_bit_cast(half8, xr[s][c]);
             }
         // the fragments are in registers: slot 1 takes its first step
+        if constexpr (STAGE == 2) __builtin_amdgcn_s_barrier();
         if (nsteps > 1) NUQ_VD_DMA(1, 1)
     } else {
 #pragma unroll
@@ -1576,60 +1581,99 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     }
 }
 
+// The LDS layout of one launch (see verify_dma_kernel).
+struct VdLayout {
+    int stage;          // 0 direct activation loads, 1 private staging, 2 shared staging
+    uint32_t region;    // per-wave stride of slot 0
+    uint32_t slot_gap;  // slot 1 - slot 0
+    uint32_t part_off;  // partial sums
+    size_t per_row;     // partial-sum bytes per row
+    size_t lds;         // for rows_per_wg rows
+};
+
 template <uint32_t ENC, uint32_t NB>
 static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
                                        uint32_t nblocks, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                        uint64_t out_stride, uint32_t tokens, uint32_t tpad, uint32_t wgs,
-                                       size_t lds, bool stage, uint32_t region, uint32_t waves) {
+                                       const VdLayout &L, uint32_t waves) {
     const dim3 grid(wgs), block(64 * waves);
-    if (x_f16 && stage)
-        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, true>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad, region);
+#define NUQ_VD_LAUNCH(XT_, MODE_)                                                                            \
+    hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_>), grid, block, L.lds, s, w, stride, rows, nblocks, \
+                       (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap, L.part_off)
+    if (x_f16 && L.stage == 1)
+        NUQ_VD_LAUNCH(_Float16, 1);
+    else if (x_f16 && L.stage == 2)
+        NUQ_VD_LAUNCH(_Float16, 2);
     else if (x_f16)
-        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, _Float16, false>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const _Float16 *)x, in_stride, y, out_stride, tokens, tpad, region);
+        NUQ_VD_LAUNCH(_Float16, 0);
     else
-        hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, float, false>), grid, block, lds, s, w, stride, rows,
-                           nblocks, (const float *)x, in_stride, y, out_stride, tokens, tpad, region);
+        NUQ_VD_LAUNCH(float, 0);
+#undef NUQ_VD_LAUNCH
     return hipGetLastError();
 }
 
-// Streams when the row's blocks fit 12 waves of 2 blocks; returns
+// Streams when the row's blocks fit 12 waves of at most 2 blocks; returns
 // false (nothing launched) otherwise.
 template <uint32_t ENC>
 static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                               const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
                               uint32_t tokens, hipError_t *err) {
-    if (rows < 16 || nblocks > 2 * vd_max_waves<2>()) return false;
-    // Runs of 2 blocks: equal work per wave and up to 3 waves per SIMD
-    // measured faster than runs of 3 (2 waves per SIMD) at K = 20 blocks.
-    const uint32_t waves = (nblocks + 1) / 2;  // the kernel's LDS layout is sized for exactly this many
+    constexpr uint32_t MAXW = vd_max_waves<2>();
+    constexpr size_t LDS = 160 * 1024;
+    if (rows < 16 || nblocks > 2 * MAXW) return false;
+    // One wave per 2 blocks: equal work per wave and up to 3 waves per SIMD.
+    // At K = 20 blocks this measured faster than 8 waves of 3 + 2 blocks per
+    // SIMD (one wave left alone on its SIMD at the end) and than 12 waves of
+    // 1 or 2 blocks (5 blocks on every SIMD, but more per-wave overhead).
+    const uint32_t waves = (nblocks + 1) / 2;
     const uint32_t tpad = (tokens + 3) & ~3u;
     const size_t slot = VDma<ENC, 2>::SLOT;
+    // wave kw's run: [kw nblocks / waves, (kw + 1) nblocks / waves)
+    uint32_t max_run = 0;
+    for (uint32_t k = 0; k < waves; ++k) max_run = std::max(max_run, (k + 1) * nblocks / waves - k * nblocks / waves);
+    const size_t xwave = (size_t)tokens * max_run * 512, xall = (size_t)tokens * nblocks * 512;
     const size_t per_row = (size_t)waves * tpad * 4;
-    // Staged f16 activations (16-byte copies: the entry points accept only
-    // 16-byte aligned rows) need tokens x 1024 bytes per wave from slot 1 on.
-    const size_t xbytes = (size_t)tokens * 2 * 512;
-    bool stage = x_f16 != 0;
-    size_t region = 2 * slot + (stage && xbytes > slot ? xbytes - slot : 0);
-    if (stage && (size_t)waves * region + 16 * per_row > 160 * 1024) {
-        stage = false;
-        region = 2 * slot;
+    // One workgroup per CU when the partial sums of its rows fit, else more,
+    // shorter row ranges; never more than rows / 16 workgroups, so each range
+    // holds at least 16 rows (the kernel's steps assume it). Ranges differ by
+    // at most one row.
+    const uint32_t want_rows = std::max(16u, (rows + 255) / 256);
+    // Candidates in order of preference: private staging, shared staging,
+    // direct loads (the only one for F32 activations); the first whose rings
+    // and partial sums hold want_rows rows, else the one holding the most.
+    VdLayout L{}, best{};
+    uint32_t best_rows = 0;
+    const int modes_f16[3] = {1, 2, 0}, modes_f32[1] = {0};
+    const int *modes = x_f16 ? modes_f16 : modes_f32;
+    for (int m = 0; m < (x_f16 ? 3 : 1); ++m) {
+        const int mode = modes[m];
+        VdLayout c{};
+        c.stage = mode;
+        c.per_row = per_row;
+        c.region = (uint32_t)(mode == 1 ? 2 * slot + (xwave > slot ? xwave - slot : 0) : mode == 2 ? slot : 2 * slot);
+        c.slot_gap = (uint32_t)(mode == 2 ? waves * slot : slot);
+        const size_t rings = mode == 2 ? 2 * waves * slot : (size_t)waves * c.region;
+        c.part_off = (uint32_t)rings;
+        if (mode == 2 && waves * slot + xall > LDS) continue;
+        if (rings + 16 * per_row > LDS) continue;
+        const uint32_t fit = (uint32_t)((LDS - rings) / per_row);
+        if (fit > best_rows) {
+            best = c;
+            best_rows = fit;
+        }
+        if (fit >= want_rows) break;
     }
-    const size_t rings = (size_t)waves * region;
-    if (rings + 16 * per_row > 160 * 1024) return false;
-    // One workgroup per CU while the partial sums fit, else more, shorter
-    // row ranges; never more than rows / 16 workgroups, so each range holds
-    // at least 16 rows (the kernel's steps assume it). Ranges differ by at
-    // most one row.
-    const uint32_t max_rows = (uint32_t)((160 * 1024 - rings) / per_row);
-    uint32_t wgs = std::max(256u, (rows + max_rows - 1) / max_rows);
+    if (best_rows < 16) return false;
+    L = best;
+    const uint32_t rings_end = L.part_off;
+    uint32_t wgs = std::max(256u, (rows + best_rows - 1) / best_rows);
     wgs = std::min(wgs, rows / 16);
     const uint32_t rows_per_wg = (rows + wgs - 1) / wgs;  // the longest range
-    if (rows_per_wg > max_rows) return false;
-    const size_t lds = rings + rows_per_wg * per_row;
+    if (rows_per_wg > best_rows) return false;
+    const size_t xall_lds = L.stage == 2 ? waves * slot + xall : 0;
+    L.lds = std::max(rings_end + rows_per_wg * L.per_row, xall_lds);
     *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, tpad,
-                                        wgs, lds, stage, (uint32_t)region, waves);
+                                        wgs, L, waves);
     return true;
 }
 

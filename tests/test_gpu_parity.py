@@ -274,11 +274,15 @@ def test_tile_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
 # The streamed verify tile (Q4_K and Q5_K, tokens <= 16, up to 24 blocks per
 # row): 2 and 3 blocks per wave, a wave whose last block is past the row
 # (odd block counts), 16-row steps that end mid-step, token counts 1..16,
-# and row ranges shortened so the partial sums fit the LDS (13, 12000, 6144,
-# 16). The weights enter the MFMAs as exact f16 integers q * sc, so only the
-# activations are rounded.
+# row ranges shortened so the partial sums fit the LDS (13, 12000, 6144,
+# 16), and the three places f16 activations go: each wave's own slot (most
+# cases), all the slot-1s behind a barrier ((12, 4096, 3840, 16),
+# (12, 8192, 4608, 12), (12, 8192, 6144, 8)), or no staging (16 tokens of
+# 24 blocks). The weights enter the MFMAs as exact f16 integers q * sc, so
+# only the activations are rounded.
 VERIFY_DMA_CASES = [(12, 17408, 5120, 8), (12, 4104, 5120, 8), (13, 1000, 4608, 16), (12, 2000, 6144, 3),
-                    (12, 808, 3840, 13), (13, 12000, 6144, 16), (12, 24, 256, 1), (13, 4104, 5120, 8)]
+                    (12, 808, 3840, 13), (13, 12000, 6144, 16), (12, 24, 256, 1), (13, 4104, 5120, 8),
+                    (12, 4096, 3840, 16), (12, 8192, 4608, 12), (12, 8192, 6144, 8)]
 
 
 @pytest.mark.parametrize("xdtype", ["f16", "f32"])
