@@ -994,6 +994,28 @@ __device__ __forceinline__ half2v f16_biased(uint32_t t) {
     return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, t, sel));
 }
 
+// Two f16 values 1024 + (t & M) from the halves of t (M keeps at most bits
+// 0-9 of each half): (t & M) | 0x64006400 as one v_and_or_b32.
+__device__ __forceinline__ half2v f16_masked(uint32_t t, uint32_t m) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(t), "s"(m), "v"(0x64006400u));
+    return __builtin_bit_cast(half2v, r);
+}
+
+// The streamed verify tile's element order within each 8-value chunk,
+// [0, 2, 1, 3, 4, 6, 5, 7]: activations go through this once per launch so
+// that the weight pairs can be built from bytes (0, 2) and (1, 3) of a code
+// word without moving bytes.
+__device__ __forceinline__ half8 vd_swizzle(half8 v) {
+    const u32x4 u = __builtin_bit_cast(u32x4, v);
+    u32x4 r;
+    r[0] = __builtin_amdgcn_perm(u[1], u[0], 0x05040100u);
+    r[1] = __builtin_amdgcn_perm(u[1], u[0], 0x07060302u);
+    r[2] = __builtin_amdgcn_perm(u[3], u[2], 0x05040100u);
+    r[3] = __builtin_amdgcn_perm(u[3], u[2], 0x07060302u);
+    return __builtin_bit_cast(half8, r);
+}
+
 // (1024 + v) * s - 1024 * s, fused (v_pk_fma_f16): v * s rounded once, and
 // exact when |v * s| <= 2048.
 __device__ __forceinline__ uint32_t scaled_codes(half2v biased, half2v s, half2v c) {
@@ -1038,8 +1060,9 @@ struct VSplit<12> {
         decode<false>(hdr, *(const uint4 *)(blk + CODE + 32 * h), *(const uint4 *)(blk + CODE + 16 + 32 * h), h, b, d,
                       nm0, nm1);
     }
-    // PAIR: the branch-free scale unpack (the streamed tile); the register
-    // tile measured faster with the per-group form
+    // PAIR: the streamed tile's form, with the branch-free scale unpack and
+    // the element order of vd_swizzle; the register tile keeps the natural
+    // order and the per-group scale unpack, which measured faster there
     template <bool PAIR>
     __device__ __forceinline__ static void decode(const uint4 (&hr)[NH], uint4 q0, uint4 q1, uint32_t h,
                                                   half8 (&b)[8], float &d, float &nm0, float &nm1) {
@@ -1069,11 +1092,19 @@ struct VSplit<12> {
             u32x4 lo, hi;
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const uint32_t l4 = w[2 * c + k] & 0x0f0f0f0fu, u4 = w[2 * c + k] & 0xf0f0f0f0u;
-                lo[2 * k] = scaled_codes(f16_biased<0, 1>(l4), S0, C0);
-                lo[2 * k + 1] = scaled_codes(f16_biased<2, 3>(l4), S0, C0);
-                hi[2 * k] = scaled_codes(f16_biased<0, 1>(u4), S1, C1);
-                hi[2 * k + 1] = scaled_codes(f16_biased<2, 3>(u4), S1, C1);
+                if constexpr (PAIR) {  // streamed order: bytes (0, 2), then (1, 3)
+                    const uint32_t w0 = w[2 * c + k], w1 = w0 >> 8;
+                    lo[2 * k] = scaled_codes(f16_masked(w0, 0x000f000fu), S0, C0);
+                    lo[2 * k + 1] = scaled_codes(f16_masked(w1, 0x000f000fu), S0, C0);
+                    hi[2 * k] = scaled_codes(f16_masked(w0, 0x00f000f0u), S1, C1);
+                    hi[2 * k + 1] = scaled_codes(f16_masked(w1, 0x00f000f0u), S1, C1);
+                } else {
+                    const uint32_t l4 = w[2 * c + k] & 0x0f0f0f0fu, u4 = w[2 * c + k] & 0xf0f0f0f0u;
+                    lo[2 * k] = scaled_codes(f16_biased<0, 1>(l4), S0, C0);
+                    lo[2 * k + 1] = scaled_codes(f16_biased<2, 3>(l4), S0, C0);
+                    hi[2 * k] = scaled_codes(f16_biased<0, 1>(u4), S1, C1);
+                    hi[2 * k + 1] = scaled_codes(f16_biased<2, 3>(u4), S1, C1);
+                }
             }
             b[c] = __builtin_bit_cast(half8, lo);
             b[c + 4] = __builtin_bit_cast(half8, hi);
@@ -1092,8 +1123,9 @@ struct VSplit<13> {
         decode<false>(hdr, *(const uint4 *)(blk + CODE + 32 * h), *(const uint4 *)(blk + CODE + 16 + 32 * h), h, b, d,
                       nm0, nm1);
     }
-    // PAIR: the branch-free scale unpack (the streamed tile); the register
-    // tile measured faster with the per-group form
+    // PAIR: the streamed tile's form, with the branch-free scale unpack and
+    // the element order of vd_swizzle; the register tile keeps the natural
+    // order and the per-group scale unpack, which measured faster there
     template <bool PAIR>
     __device__ __forceinline__ static void decode(const uint4 (&hr)[NH], uint4 q0, uint4 q1, uint32_t h,
                                                   half8 (&b)[8], float &d, float &nm0, float &nm1) {
@@ -1126,10 +1158,11 @@ struct VSplit<13> {
                 const uint32_t wd = w[2 * c + k], hd = hb[2 * c + k];
                 const uint32_t l5 = (wd & 0x0f0f0f0fu) | (((hd >> (2 * h)) & 0x01010101u) << 4);
                 const uint32_t u5 = ((wd >> 4) & 0x0f0f0f0fu) | (((hd >> (2 * h + 1)) & 0x01010101u) << 4);
-                lo[2 * k] = scaled_codes(f16_biased<0, 1>(l5), S0, C0);
-                lo[2 * k + 1] = scaled_codes(f16_biased<2, 3>(l5), S0, C0);
-                hi[2 * k] = scaled_codes(f16_biased<0, 1>(u5), S1, C1);
-                hi[2 * k + 1] = scaled_codes(f16_biased<2, 3>(u5), S1, C1);
+                constexpr int A0 = PAIR ? 0 : 0, A1 = PAIR ? 2 : 1, B0 = PAIR ? 1 : 2, B1 = 3;  // streamed order
+                lo[2 * k] = scaled_codes(f16_biased<A0, A1>(l5), S0, C0);
+                lo[2 * k + 1] = scaled_codes(f16_biased<B0, B1>(l5), S0, C0);
+                hi[2 * k] = scaled_codes(f16_biased<A0, A1>(u5), S1, C1);
+                hi[2 * k + 1] = scaled_codes(f16_biased<B0, B1>(u5), S1, C1);
             }
             b[c] = __builtin_bit_cast(half8, lo);
             b[c + 4] = __builtin_bit_cast(half8, hi);
@@ -1508,6 +1541,11 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
             }
         }
     }
+
+#pragma unroll
+    for (uint32_t s = 0; s < NB; ++s)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) bx[s][c] = vd_swizzle(bx[s][c]);
 
     // F32 sums of the f16 activations of groups 2h and 2h+1 of each block
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
