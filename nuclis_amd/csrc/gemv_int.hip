@@ -47,6 +47,7 @@ struct XSlice {
     float sum;
     int isum;      // sum of x16 (used by biased codes)
     float poison;  // NaN when the slice holds a non-finite value, else 0
+    int hsum;      // sum of x16 over values 0-15 (Q6_K's 16-value scales; registers only)
 };
 
 // LDS image of one quantised slice: 16 plane dwords + scale, sum, isum, poison.
@@ -539,31 +540,34 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
         const uint32_t la[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
         const uint32_t lb[8] = {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w};
         const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        const uint32_t ls = 4 * (j & 1), hs = 4 * (j & 1);
+        // Codes stay unsigned (0..63, also valid signed bytes); the -32 bias
+        // comes off each 16-value sum as 32 * sum(x16), so every integer
+        // below is the same as with the biased codes.
+        const uint32_t sh = 4 * (j & 1);
         int a0h = 0, a0l = 0, a1h = 0, a1l = 0, b0h = 0, b0l = 0, b1h = 0, b1l = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t ua = ((la[k] >> ls) & 0x0f0f0f0fu) | (((hb[k] >> hs) & 0x03030303u) << 4);
-            const uint32_t ub = ((lb[k] >> ls) & 0x0f0f0f0fu) | (((hb[k] >> (hs + 2)) & 0x03030303u) << 4);
-            // u - 32 per byte as a signed byte, without borrows between bytes
-            const uint32_t sa = ((ua | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-            const uint32_t sb = ((ub | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            const uint32_t hq = hb[k] >> sh;
+            const uint32_t ua = ((la[k] >> sh) & 0x0f0f0f0fu) | ((hq << 4) & 0x30303030u);
+            const uint32_t ub = ((lb[k] >> sh) & 0x0f0f0f0fu) | ((hq << 2) & 0x30303030u);
             if (k < 4) {
-                a0h = dot4(sa, A.hi[k], a0h);
-                a0l = dot4(sa, A.lo[k], a0l);
-                b0h = dot4(sb, B.hi[k], b0h);
-                b0l = dot4(sb, B.lo[k], b0l);
+                a0h = dot4(ua, A.hi[k], a0h);
+                a0l = dot4(ua, A.lo[k], a0l);
+                b0h = dot4(ub, B.hi[k], b0h);
+                b0l = dot4(ub, B.lo[k], b0l);
             } else {
-                a1h = dot4(sa, A.hi[k], a1h);
-                a1l = dot4(sa, A.lo[k], a1l);
-                b1h = dot4(sb, B.hi[k], b1h);
-                b1l = dot4(sb, B.lo[k], b1l);
+                a1h = dot4(ua, A.hi[k], a1h);
+                a1l = dot4(ua, A.lo[k], a1l);
+                b1h = dot4(ub, B.hi[k], b1h);
+                b1l = dot4(ub, B.lo[k], b1l);
             }
         }
         const float s0 = (float)(int8_t)(sc & 0xffu), s1 = (float)(int8_t)((sc >> 8) & 0xffu);
         const float s2 = (float)(int8_t)((sc >> 16) & 0xffu), s3 = (float)(int8_t)(sc >> 24);
-        const float ta = fmaf(s0, (float)(a0h * 256 + a0l), s1 * (float)(a1h * 256 + a1l));
-        const float tb = fmaf(s2, (float)(b0h * 256 + b0l), s3 * (float)(b1h * 256 + b1l));
+        const int ia0 = a0h * 256 + a0l - 32 * A.hsum, ia1 = a1h * 256 + a1l - 32 * (A.isum - A.hsum);
+        const int ib0 = b0h * 256 + b0l - 32 * B.hsum, ib1 = b1h * 256 + b1l - 32 * (B.isum - B.hsum);
+        const float ta = fmaf(s0, (float)ia0, s1 * (float)ia1);
+        const float tb = fmaf(s2, (float)ib0, s3 * (float)ib1);
         return half_bits(d16) * fmaf(A.scale, ta, B.scale * tb);
     }
 };
@@ -797,6 +801,19 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
     const uint32_t bb = live ? b : 0;
     read_slice_asm(slices + (bb * 8 + 2 * j) * SLICE_WORDS, xa);
     read_slice_asm(slices + (bb * 8 + 2 * j + 1) * SLICE_WORDS, xb);
+    if constexpr (ENC == 14) {
+        // sum of x16 = 256 xh + xl over values 0-15 (the first 4 plane dwords)
+        int ha = 0, la_ = 0, hb_ = 0, lb_ = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            ha = dot4(xa.hi[k], 0x01010101u, ha);
+            la_ = dot4(xa.lo[k], 0x01010101u, la_);
+            hb_ = dot4(xb.hi[k], 0x01010101u, hb_);
+            lb_ = dot4(xb.lo[k], 0x01010101u, lb_);
+        }
+        xa.hsum = ha * 256 + la_;
+        xb.hsum = hb_ * 256 + lb_;
+    }
     if (!live) {
         xa.scale = xb.scale = 0.f;
         xa.sum = xb.sum = 0.f;
