@@ -474,7 +474,9 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
     // Blocks sit at 2-byte offsets in the ring. Misaligned LDS reads return
     // the right bytes but stall, so the fields are read as 4-byte aligned
     // dword pairs one dword longer than needed and shifted into place with
-    // v_alignbyte_b32 (by 0 or 2 bytes, the block's offset mod 4).
+    // one funnel shift each (v_alignbit_b32): by the block's offset mod 4
+    // in bytes, plus 4 bits for the lanes that take the high nibbles (and
+    // the matching high-bit pairs), so the code words need no other shift.
     template <int VM>
     __device__ __forceinline__ void read(const uint8_t *blk, uint32_t j) {
         typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
@@ -519,10 +521,11 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
             t[2 * k + 1] = hq[k].y;
         }
         uint32_t o[16], p[8];
+        const uint32_t bits = 8 * sh + 4 * (j & 1);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) o[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], sh);
+        for (int k = 0; k < 16; ++k) o[k] = __builtin_amdgcn_alignbit(r[k + 1], r[k], bits);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) p[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+        for (int k = 0; k < 8; ++k) p[k] = __builtin_amdgcn_alignbit(t[k + 1], t[k], bits);
         l0 = u32x4_t{o[0], o[1], o[2], o[3]};
         l1 = u32x4_t{o[4], o[5], o[6], o[7]};
         l2 = u32x4_t{o[8], o[9], o[10], o[11]};
@@ -535,21 +538,21 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
     // lane j: quarters q0 = 2(j&1) (x slice A) and q0+1 (slice B) of half
     // j>>1; code of column c = nibble j&1 of ql[c] (ql[32 + c] for q0+1) |
     // bits 2q of qh[c] as bits 4-5, minus 32 (quant/decode.zig:198-211);
-    // scale bytes: A columns 0-15, 16-31, then B's.
-    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t, bool) const {
+    // scale bytes: A columns 0-15, 16-31, then B's. read() has already
+    // shifted the code and high-bit words by 4 (j&1) bits.
+    __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t, uint32_t, bool) const {
         const uint32_t la[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
         const uint32_t lb[8] = {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w};
         const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         // Codes stay unsigned (0..63, also valid signed bytes); the -32 bias
         // comes off each 16-value sum as 32 * sum(x16), so every integer
         // below is the same as with the biased codes.
-        const uint32_t sh = 4 * (j & 1);
         int a0h = 0, a0l = 0, a1h = 0, a1l = 0, b0h = 0, b0l = 0, b1h = 0, b1l = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t hq = hb[k] >> sh;
-            const uint32_t ua = ((la[k] >> sh) & 0x0f0f0f0fu) | ((hq << 4) & 0x30303030u);
-            const uint32_t ub = ((lb[k] >> sh) & 0x0f0f0f0fu) | ((hq << 2) & 0x30303030u);
+            const uint32_t hq = hb[k];
+            const uint32_t ua = (la[k] & 0x0f0f0f0fu) | ((hq << 4) & 0x30303030u);
+            const uint32_t ub = (lb[k] & 0x0f0f0f0fu) | ((hq << 2) & 0x30303030u);
             if (k < 4) {
                 a0h = dot4(ua, A.hi[k], a0h);
                 a0l = dot4(ua, A.lo[k], a0l);
