@@ -124,6 +124,9 @@ GEMV_SHAPES = [
     (12, 257, 1024),      # one wave set, ragged last workgroup
     (12, 100, 24576),     # 8-block lane groups on the DMA kernel
     (12, 64, 32768),      # x and the rings exceed LDS: register kernel
+    (12, 5120, 17408),    # the down projection (8-block lane groups)
+    (12, 37, 16640),      # 65 blocks: a partial last lane group, ragged rows
+    (12, 300, 17408),
     (13, 1024, 5120),     # Q5_K and IQ4_XS
     (23, 1024, 5120),
     (13, 35, 1280),
