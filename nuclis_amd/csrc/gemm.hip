@@ -1425,15 +1425,24 @@ __device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
 }
 
 template <uint32_t ENC, uint32_t NB, typename XT, int STAGE>
-__global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w,
+__global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w_all,
                                                                         uint64_t stride, uint32_t rows,
-                                                                        uint32_t nblocks, const XT *__restrict__ x,
-                                                                        uint64_t in_stride, float *__restrict__ y,
+                                                                        uint32_t nblocks_all,
+                                                                        const XT *__restrict__ x_all,
+                                                                        uint64_t in_stride, float *__restrict__ y_all,
                                                                         uint64_t out_stride, uint32_t tokens,
                                                                         uint32_t tpad, uint32_t region,
-                                                                        uint32_t slot_gap, uint32_t part_off) {
+                                                                        uint32_t slot_gap, uint32_t part_off,
+                                                                        uint32_t kb, uint64_t y_range) {
     using L = VSplit<ENC>;
     using V = VDma<ENC, NB>;
+    // K ranges (gridDim.y > 1): workgroup (bx, by) takes blocks
+    // [by kb, (by + 1) kb) and stores its sums y_range floats further on
+    const uint32_t kb0 = blockIdx.y * kb;
+    const uint32_t nblocks = gridDim.y > 1 ? min(kb, nblocks_all - kb0) : nblocks_all;
+    const uint8_t *__restrict__ w = w_all + (uint64_t)kb0 * L::BLOCK_BYTES;
+    const XT *__restrict__ x = x_all + (uint64_t)kb0 * L::BLOCK_VALUES;
+    float *__restrict__ y = y_all + blockIdx.y * y_range;
     extern __shared__ __attribute__((aligned(16))) uint8_t vd_lds[];
     const uint32_t lane = threadIdx.x & 63, kw = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t r16 = lane & 15, h = lane >> 4;
@@ -1633,11 +1642,13 @@ template <uint32_t ENC, uint32_t NB>
 static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
                                        uint32_t nblocks, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                        uint64_t out_stride, uint32_t tokens, uint32_t tpad, uint32_t wgs,
-                                       const VdLayout &L, uint32_t waves) {
-    const dim3 grid(wgs), block(64 * waves);
+                                       const VdLayout &L, uint32_t waves, uint32_t ranges, uint32_t kb,
+                                       uint64_t y_range) {
+    const dim3 grid(wgs, ranges), block(64 * waves);
 #define NUQ_VD_LAUNCH(XT_, MODE_)                                                                            \
     hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_>), grid, block, L.lds, s, w, stride, rows, nblocks, \
-                       (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap, L.part_off)
+                       (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap, L.part_off, kb,   \
+                       y_range)
     if (x_f16 && L.stage == 1)
         NUQ_VD_LAUNCH(_Float16, 1);
     else if (x_f16 && L.stage == 2)
@@ -1650,15 +1661,42 @@ static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t
     return hipGetLastError();
 }
 
-// Streams when the row's blocks fit 12 waves of at most 2 blocks; returns
-// false (nothing launched) otherwise.
+// Adds the K ranges' partial sums in range order: y[t][r] = sum over k of
+// ws[k][t][r] (ws rows x tokens per range, rows contiguous).
+__global__ void verify_reduce_kernel(const float *__restrict__ ws, uint32_t nranges, uint32_t rows, uint32_t tokens,
+                                     float *__restrict__ y, uint64_t out_stride) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * tokens) return;
+    const uint32_t t = i / rows, r = i - t * rows;
+    float v = 0.f;
+    for (uint32_t k = 0; k < nranges; ++k) v += ws[((uint64_t)k * tokens + t) * rows + r];
+    y[(uint64_t)t * out_stride + r] = v;
+}
+
+// Streams when the row's blocks fit 12 waves of at most 2 blocks, or, with a
+// workspace, in K ranges of at most 24 blocks whose sums verify_reduce_kernel
+// adds; returns false (nothing launched) otherwise.
 template <uint32_t ENC>
-static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
-                              const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
-                              uint32_t tokens, hipError_t *err) {
+static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks_all,
+                              const void *x, uint32_t x_f16, uint64_t in_stride, float *y_out,
+                              uint64_t out_stride_out, uint32_t tokens, hipError_t *err,
+                              const SplitScratch *scratch = nullptr) {
     constexpr uint32_t MAXW = vd_max_waves<2>();
     constexpr size_t LDS = 160 * 1024;
-    if (rows < 16 || nblocks > 2 * MAXW) return false;
+    if (rows < 16) return false;
+    // K ranges: longer rows (the down projection) run as `ranges` ranges of
+    // kb blocks over the workgroups, into the prefill workspace
+    uint32_t ranges = 1, kb = nblocks_all;
+    if (nblocks_all > 2 * MAXW) {
+        ranges = (nblocks_all + 2 * MAXW - 1) / (2 * MAXW);
+        kb = (nblocks_all + ranges - 1) / ranges;
+        if (!scratch || !scratch->work ||
+            (uint64_t)ranges * tokens * rows > (uint64_t)scratch->tiles * 256 * 256)
+            return false;
+    }
+    const uint32_t nblocks = kb;
+    float *y = ranges > 1 ? scratch->work : y_out;
+    const uint64_t out_stride = ranges > 1 ? rows : out_stride_out;
     // One wave per 2 blocks: equal work per wave and up to 3 waves per SIMD.
     // At K = 20 blocks this measured faster than 8 waves of 3 + 2 blocks per
     // SIMD (one wave left alone on its SIMD at the end) and than 12 waves of
@@ -1675,7 +1713,7 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // shorter row ranges; never more than rows / 16 workgroups, so each range
     // holds at least 16 rows (the kernel's steps assume it). Ranges differ by
     // at most one row.
-    const uint32_t want_rows = std::max(16u, (rows + 255) / 256);
+    const uint32_t want_rows = std::max(16u, (rows * ranges + 255) / 256);
     // Candidates in order of preference: private staging, shared staging,
     // direct loads (the only one for F32 activations); the first whose rings
     // and partial sums hold want_rows rows, else the one holding the most.
@@ -1704,14 +1742,20 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     if (best_rows < 16) return false;
     L = best;
     const uint32_t rings_end = L.part_off;
-    uint32_t wgs = std::max(256u, (rows + best_rows - 1) / best_rows);
+    uint32_t wgs = std::max(std::max(1u, 256 / ranges), (rows + best_rows - 1) / best_rows);
     wgs = std::min(wgs, rows / 16);
     const uint32_t rows_per_wg = (rows + wgs - 1) / wgs;  // the longest range
     if (rows_per_wg > best_rows) return false;
     const size_t xall_lds = L.stage == 2 ? waves * slot + xall : 0;
     L.lds = std::max(rings_end + rows_per_wg * L.per_row, xall_lds);
-    *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, tpad,
-                                        wgs, L, waves);
+    *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks_all, x, x_f16, in_stride, y, out_stride, tokens,
+                                        tpad, wgs, L, waves, ranges, kb, (uint64_t)tokens * rows);
+    if (*err == hipSuccess && ranges > 1) {
+        const uint32_t n = rows * tokens;
+        hipLaunchKernelGGL(verify_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, scratch->work, ranges, rows,
+                           tokens, y_out, out_stride_out);
+        *err = hipGetLastError();
+    }
     return true;
 }
 
@@ -1741,11 +1785,12 @@ static hipError_t launch_verify_rg(hipStream_t s, const uint8_t *w, uint64_t str
 template <uint32_t ENC>
 static hipError_t launch_verify_enc(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows,
                                     uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
-                                    uint64_t out_stride, uint32_t tokens) {
+                                    uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch) {
     const uint32_t nblocks = columns / 256;
     if constexpr (ENC == 12 || ENC == 13) {
         hipError_t err;
-        if (launch_verify_dma<ENC>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, &err))
+        if (launch_verify_dma<ENC>(s, w, stride, rows, nblocks, x, x_f16, in_stride, y, out_stride, tokens, &err,
+                                   &scratch))
             return err;
     }
     // About five blocks per wave (at most VF_MAX_WAVES waves), split evenly:
@@ -1781,11 +1826,11 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch) {
     if (tokens <= 16 && columns % 256 == 0) {
         switch (encoding) {
-        case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        case 13: return launch_verify_enc<13>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        case 14: return launch_verify_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        case 23: return launch_verify_enc<23>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
-        default: return launch_verify_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens);
+        case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
+        case 13: return launch_verify_enc<13>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
+        case 14: return launch_verify_enc<14>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
+        case 23: return launch_verify_enc<23>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
+        default: return launch_verify_enc<8>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
         }
     }
     // (the prefill tile's activation copies use 32-bit offsets within a tile)

@@ -281,11 +281,13 @@ def test_tile_matches_oracle(backend, encoding, rows, columns, tokens, xdtype):
 # 16), and the three places f16 activations go: each wave's own slot (most
 # cases), all the slot-1s behind a barrier ((12, 4096, 3840, 16),
 # (12, 8192, 4608, 12), (12, 8192, 6144, 8)), or no staging (16 tokens of
-# 24 blocks). The weights enter the MFMAs as exact f16 integers q * sc, so
-# only the activations are rounded.
+# 24 blocks), and rows longer than 24 blocks in K ranges. The weights enter
+# the MFMAs as exact f16 integers q * sc, so only the activations are rounded.
 VERIFY_DMA_CASES = [(12, 17408, 5120, 8), (12, 4104, 5120, 8), (13, 1000, 4608, 16), (12, 2000, 6144, 3),
                     (12, 808, 3840, 13), (13, 12000, 6144, 16), (12, 24, 256, 1), (13, 4104, 5120, 8),
-                    (12, 4096, 3840, 16), (12, 8192, 4608, 12), (12, 8192, 6144, 8)]
+                    (12, 4096, 3840, 16), (12, 8192, 4608, 12), (12, 8192, 6144, 8),
+                    # rows longer than 24 blocks: K ranges added by a second kernel
+                    (12, 5120, 17408, 8), (13, 1040, 17408, 16), (12, 2000, 12544, 5)]
 
 
 @pytest.mark.parametrize("xdtype", ["f16", "f32"])
@@ -327,7 +329,8 @@ def test_streamed_verify_strided_activations(backend, pad):
         backend.matmul_kernel(nq.KERNEL_TILE, m, odd, columns + 4, out, rows, tokens)
 
 
-@pytest.mark.parametrize("encoding,rows,columns,tokens", [(12, 5120, 17408, 512), (14, 2048, 5120, 1024), (12, 17408, 5120, 8)])
+@pytest.mark.parametrize("encoding,rows,columns,tokens", [(12, 5120, 17408, 512), (14, 2048, 5120, 1024), (12, 17408, 5120, 8),
+                                                       (12, 5120, 17408, 8)])
 def test_prefill_split_k_is_deterministic(backend, encoding, rows, columns, tokens):
     """Tiles split along K are summed in split order by whichever split
     finishes last: repeated launches must agree bit for bit."""
