@@ -14,6 +14,7 @@
 // fragment is one 16-byte LDS read. Rows are padded by 8 halves to spread
 // the 32 rows of a fragment over the LDS banks.
 #include <algorithm>
+#include <type_traits>
 
 #include "formats.h"
 #include "kernels.h"
@@ -1405,6 +1406,44 @@ __device__ __forceinline__ void vd_ring_read(uint32_t a, uint32_t c, uint4 (&hd)
     }
 }
 
+// The arithmetic of one streamed-verify step over NL live blocks: per
+// block an independent chain of eight f16 MFMAs against q * sc, scaled by
+// the block's d, plus one chain of F32 MFMAs for the minimum terms.
+template <typename L, uint32_t NB, uint32_t NL>
+__device__ __forceinline__ floatx4 vd_step_blocks(const uint4 (&hd)[NB][L::NH], const uint4 (&cq)[NB][2], uint32_t h,
+                                                  const half8 (&bx)[NB][8], const float (&sx)[NB][2]) {
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    floatx4 part[NL], accm = zero;
+    float d[NL];
+#pragma unroll
+    for (uint32_t s = 0; s < NL; ++s) {
+        half8 bq[8];
+        float nm0, nm1;
+        L::template decode<true>(hd[s], cq[s][0], cq[s][1], h, bq, d[s], nm0, nm1);
+        part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][0], bq[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int c = 1; c < 8; ++c) part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][c], bq[c], part[s], 0, 0, 0);
+        accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][0], nm0, accm, 0, 0, 0);
+        accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][1], nm1, accm, 0, 0, 0);
+    }
+    floatx4 acc = accm;
+#pragma unroll
+    for (uint32_t s = 0; s < NL; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(d[s], part[s][e], acc[e]);
+    return acc;
+}
+
+// One 16-byte-per-lane copy global -> LDS as a buffer load: base in a
+// buffer resource (scalar), lane offset voff, uniform offset soff, LDS
+// destination lds (uniform, the lane's 16 bytes at lds + 16 lane), with the
+// non-temporal hint. The record count is the maximum: callers keep every
+// offset inside their rows.
+__device__ __forceinline__ void vd_copy(const uint8_t *base, uint32_t lds, uint32_t voff, uint32_t soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, 0xffffffff, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(uintptr_t)lds, 16, voff, soff, 0, 2);
+}
+
 // Fragment reads of one block of staged activations: the lane's 128
 // contiguous bytes at a + O (chunks c = 0..7 at 16 c). No wait.
 template <uint32_t O>
@@ -1475,13 +1514,18 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
                   (sblk < nlive ? in_row : in_row - sblk * V::BYTES);
     }
     const uint8_t *wg_base = w + (uint64_t)row_begin * stride;
+    // The copies run as buffer loads: the workgroup's base in a buffer
+    // resource, the step's row offset as the scalar offset and the lane's
+    // fixed 32-bit offset, so a copy costs no VALU. Every offset stays in
+    // the workgroup's rows, so the record count is left at its maximum.
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(vd_lds_addr(ring));
 #define NUQ_VD_DMA(SLOT_, STEP_)                                                                          \
     {                                                                                                   \
-        const uint8_t *sbase_ = wg_base + (uint64_t)min(16 * (STEP_), nrow - 16) * stride;              \
+        const uint32_t soff_ = min(16 * (STEP_), nrow - 16) * (uint32_t)stride;                         \
+        const uint32_t dst_ = ring_lds + (SLOT_) * slot_stride;                                         \
         _Pragma("unroll") for (uint32_t n = 0; n < V::INSTRS; ++n) {                                    \
             if (64 * (n + 1) <= V::STEP_CHUNKS || 64 * n + lane < V::STEP_CHUNKS)                          \
-                __builtin_amdgcn_global_load_lds((global_void_t *)(sbase_ + doff[n]),                     \
-                                                 (lds_void_t *)(ring + (SLOT_) * slot_stride + n * 1024), 16, 0, 2); \
+                vd_copy(wg_base, dst_ + n * 1024, doff[n], soff_);                                      \
         }                                                                                               \
     }
     half8 bx[NB][8];
@@ -1587,29 +1631,11 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         else
             vd_ring_read<ENC, NB, 0>(a, a + L::CODE + 32 * h, hd, cq);
         if (i + VD_DEPTH < nsteps) NUQ_VD_DMA(slot, i + VD_DEPTH)
-        // independent MFMA chains: one per block, one for the minimum terms
-        floatx4 part[NB], accm = zero;
-        float d[NB];
-#pragma unroll
-        for (uint32_t s = 0; s < NB; ++s) {
-            if (s >= nlive) break;
-            half8 bq[8];
-            float nm0, nm1;
-            L::template decode<true>(hd[s], cq[s][0], cq[s][1], h, bq, d[s], nm0, nm1);
-            part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][0], bq[0], zero, 0, 0, 0);
-#pragma unroll
-            for (int c = 1; c < 8; ++c)
-                part[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[s][c], bq[c], part[s], 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][0], nm0, accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[s][1], nm1, accm, 0, 0, 0);
-        }
-        floatx4 acc = accm;
-#pragma unroll
-        for (uint32_t s = 0; s < NB; ++s) {
-            if (s >= nlive) break;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(d[s], part[s][e], acc[e]);
-        }
+        // one copy of the step body per live block count (wave-uniform), so
+        // the per-block results need no merging
+        static_assert(NB == 2, "live block counts 1 and 2");
+        const floatx4 acc = nlive == NB ? vd_step_blocks<L, NB, NB>(hd, cq, h, bx, sx)
+                                        : vd_step_blocks<L, NB, 1>(hd, cq, h, bx, sx);
         // D: lane holds row base + r16 (base = min(16 i, nrow - 16)), tokens
         // 4h..4h+3; rows an earlier step stored are skipped (written through
         // asm: the compiler would otherwise wait for every ring copy in flight)
