@@ -170,15 +170,16 @@ __device__ __forceinline__ float decode_value(uint32_t encoding, const uint8_t *
 // IQ4_XS / IQ4_NL code lookup for four codes at once: byte e of `codes`
 // (0..15) -> byte e of the result = kIq4Values[code] as a signed byte. Two
 // v_perm_b32 pick from table entries 0-7 and 8-15 (selectors 0-7 address the
-// eight bytes of a dword pair, low dword first) and bit 3 of each code
-// chooses between them.
+// eight bytes of a dword pair, low dword first); a third picks byte e of
+// the second when bit 3 of code e is set (selector e + 4), else of the first
+// (selector e).
 __device__ __forceinline__ uint32_t iq4_lookup(uint32_t codes) {
     // entries 0-3, 4-7, 8-11, 12-15 of kIq4Values as little-endian bytes
     constexpr uint32_t T0 = 0xbfad9881u, T1 = 0xf6eaddcfu, T2 = 0x26190d01u, T3 = 0x71594535u;
     const uint32_t sel = codes & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
-    const uint32_t mask = ((codes >> 3) & 0x01010101u) * 0xffu;
-    return (hi & mask) | (lo & ~mask);
+    const uint32_t pick = ((codes >> 1) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
 // Byte E of a dword as a signed value in F32.
