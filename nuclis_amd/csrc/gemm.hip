@@ -1333,7 +1333,6 @@ __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_split_kernel(const u
 //   2:    every wave's slot 0, every wave's slot 1, the partial sums; the
 //         activations are staged over the slot-1s and partial sums, so a
 //         barrier separates the fragment reads from the step-1 copies.
-constexpr uint32_t VD_DEPTH = 2;     // ring slots per wave
 // waves per workgroup: runs of 2 blocks fit 170 registers (3 waves per
 // SIMD), runs of 3 need 256 (2 per SIMD)
 template <uint32_t NB>
@@ -1463,7 +1462,7 @@ __device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
         : "memory");
 }
 
-template <uint32_t ENC, uint32_t NB, typename XT, int STAGE>
+template <uint32_t ENC, uint32_t NB, typename XT, int STAGE, uint32_t DEPTH>
 __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w_all,
                                                                         uint64_t stride, uint32_t rows,
                                                                         uint32_t nblocks_all,
@@ -1532,12 +1531,14 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     if constexpr (STAGE != 0) {
         // this wave's activations, [token][its blocks' 512 bytes], copied
         // before the step-0 weights so that they are waited for alone
+        static_assert(NB <= 2, "a run's activations are 32 or 64 chunks per token");
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
+        const uint32_t span_log2 = nlive == 2 ? 6 : 5;  // log2(span / 16)
         uint8_t *xs = STAGE == 1 ? ring + V::SLOT : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
         for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
             const uint32_t k = 64 * jx + lane;
             if (k < xchunks) {
-                const uint32_t t = k / (span / 16), rem = k - t * (span / 16);
+                const uint32_t t = k >> span_log2, rem = k & ((1u << span_log2) - 1);
                 const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
                 __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(xs + 1024 * jx), 16, 0, 0);
             }
@@ -1561,12 +1562,14 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
                 asm volatile("" : "+v"(xr[s][c]));
                 bx[s][c] = __builtin_bit_cast(half8, xr[s][c]);
             }
-        // the fragments are in registers: slot 1 takes its first step
+        // the fragments are in registers: slots 1.. take their first steps
         if constexpr (STAGE == 2) __builtin_amdgcn_s_barrier();
-        if (nsteps > 1) NUQ_VD_DMA(1, 1)
+#pragma unroll
+        for (uint32_t d = 1; d < DEPTH; ++d)
+            if (d < nsteps) NUQ_VD_DMA(d, d)
     } else {
 #pragma unroll
-        for (uint32_t d = 0; d < VD_DEPTH; ++d)
+        for (uint32_t d = 0; d < DEPTH; ++d)
             if (d < nsteps) NUQ_VD_DMA(d, d)
 
         // x fragments of the wave's blocks, loaded after the first copies are
@@ -1621,16 +1624,20 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     const uint32_t part_a = vd_lds_addr((const uint8_t *)partial) + ((r16 * nwaves + kw) * tpad + 4 * h) * 4;
     const uint32_t part_step = 16 * nwaves * tpad * 4;
     const bool store_tokens = 4 * h < tpad;
+    uint32_t slot = 0;  // i % DEPTH
     for (uint32_t i = 0; i < nsteps; ++i) {
-        const uint32_t slot = i & (VD_DEPTH - 1);
         uint4 hd[NB][L::NH], cq[NB][2];
         const uint32_t a = ring_a + slot * slot_stride;
-        // the next step's copies may still be in flight, except on the last
-        if (i + 1 < nsteps)
+        // the copies of up to DEPTH - 1 younger steps may still be in flight
+        const uint32_t ahead = min(DEPTH - 1, nsteps - 1 - i);
+        if (DEPTH > 2 && ahead >= 2)
+            vd_ring_read<ENC, NB, 2 * V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
+        else if (ahead >= 1)
             vd_ring_read<ENC, NB, V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
         else
             vd_ring_read<ENC, NB, 0>(a, a + L::CODE + 32 * h, hd, cq);
-        if (i + VD_DEPTH < nsteps) NUQ_VD_DMA(slot, i + VD_DEPTH)
+        if (i + DEPTH < nsteps) NUQ_VD_DMA(slot, i + DEPTH)
+        slot = slot + 1 == DEPTH ? 0 : slot + 1;
         // one copy of the step body per live block count (wave-uniform), so
         // the per-block results need no merging
         static_assert(NB == 2, "live block counts 1 and 2");
@@ -1657,6 +1664,7 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
 // The LDS layout of one launch (see verify_dma_kernel).
 struct VdLayout {
     int stage;          // 0 direct activation loads, 1 private staging, 2 shared staging
+    uint32_t depth;     // ring slots per wave (2 or 3)
     uint32_t region;    // per-wave stride of slot 0
     uint32_t slot_gap;  // slot 1 - slot 0
     uint32_t part_off;  // partial sums
@@ -1671,18 +1679,25 @@ static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t
                                        const VdLayout &L, uint32_t waves, uint32_t ranges, uint32_t kb,
                                        uint64_t y_range) {
     const dim3 grid(wgs, ranges), block(64 * waves);
-#define NUQ_VD_LAUNCH(XT_, MODE_)                                                                            \
-    hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_>), grid, block, L.lds, s, w, stride, rows, nblocks, \
-                       (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap, L.part_off, kb,   \
-                       y_range)
-    if (x_f16 && L.stage == 1)
-        NUQ_VD_LAUNCH(_Float16, 1);
-    else if (x_f16 && L.stage == 2)
-        NUQ_VD_LAUNCH(_Float16, 2);
-    else if (x_f16)
-        NUQ_VD_LAUNCH(_Float16, 0);
-    else
-        NUQ_VD_LAUNCH(float, 0);
+#define NUQ_VD_LAUNCH(XT_, MODE_, D_)                                                                        \
+    hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_, D_>), grid, block, L.lds, s, w, stride, rows,    \
+                       nblocks, (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap,      \
+                       L.part_off, kb, y_range)
+#define NUQ_VD_LAUNCH_D(XT_, MODE_)                                                                          \
+    if (L.depth == 3)                                                                                       \
+        NUQ_VD_LAUNCH(XT_, MODE_, 3);                                                                       \
+    else                                                                                                    \
+        NUQ_VD_LAUNCH(XT_, MODE_, 2);
+    if (x_f16 && L.stage == 1) {
+        NUQ_VD_LAUNCH_D(_Float16, 1)
+    } else if (x_f16 && L.stage == 2) {
+        NUQ_VD_LAUNCH_D(_Float16, 2)
+    } else if (x_f16) {
+        NUQ_VD_LAUNCH_D(_Float16, 0)
+    } else {
+        NUQ_VD_LAUNCH_D(float, 0)
+    }
+#undef NUQ_VD_LAUNCH_D
 #undef NUQ_VD_LAUNCH
     return hipGetLastError();
 }
@@ -1743,27 +1758,43 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // Candidates in order of preference: private staging, shared staging,
     // direct loads (the only one for F32 activations); the first whose rings
     // and partial sums hold want_rows rows, else the one holding the most.
+    // Candidates in order of preference: three ring slots (two steps in
+    // flight while one computes), then two; within each, private staging,
+    // shared staging, direct loads (the only one for F32 activations). The
+    // first whose rings and partial sums hold want_rows rows wins, else the
+    // one holding the most.
     VdLayout L{}, best{};
     uint32_t best_rows = 0;
     const int modes_f16[3] = {1, 2, 0}, modes_f32[1] = {0};
     const int *modes = x_f16 ? modes_f16 : modes_f32;
-    for (int m = 0; m < (x_f16 ? 3 : 1); ++m) {
-        const int mode = modes[m];
-        VdLayout c{};
-        c.stage = mode;
-        c.per_row = per_row;
-        c.region = (uint32_t)(mode == 1 ? 2 * slot + (xwave > slot ? xwave - slot : 0) : mode == 2 ? slot : 2 * slot);
-        c.slot_gap = (uint32_t)(mode == 2 ? waves * slot : slot);
-        const size_t rings = mode == 2 ? 2 * waves * slot : (size_t)waves * c.region;
-        c.part_off = (uint32_t)rings;
-        if (mode == 2 && waves * slot + xall > LDS) continue;
-        if (rings + 16 * per_row > LDS) continue;
-        const uint32_t fit = (uint32_t)((LDS - rings) / per_row);
-        if (fit > best_rows) {
-            best = c;
-            best_rows = fit;
+    bool found = false;
+    for (uint32_t depth = 3; depth >= 2 && !found; --depth) {
+        for (int m = 0; m < (x_f16 ? 3 : 1); ++m) {
+            const int mode = modes[m];
+            VdLayout c{};
+            c.stage = mode;
+            c.depth = depth;
+            c.per_row = per_row;
+            const size_t ahead = (depth - 1) * slot;  // staging room from slot 1 on
+            c.region = (uint32_t)(mode == 1 ? depth * slot + (xwave > ahead ? xwave - ahead : 0)
+                                            : mode == 2 ? slot : depth * slot);
+            c.slot_gap = (uint32_t)(mode == 2 ? waves * slot : slot);
+            const size_t rings = mode == 2 ? depth * waves * slot : (size_t)waves * c.region;
+            c.part_off = (uint32_t)rings;
+            if (mode == 2 && waves * slot + xall > LDS) continue;
+            if (rings + 16 * per_row > LDS) continue;
+            const uint32_t fit = (uint32_t)((LDS - rings) / per_row);
+            if (fit > best_rows) {
+                best = c;
+                best_rows = fit;
+            }
+            if (fit >= want_rows) {
+                best = c;
+                best_rows = fit;
+                found = true;
+                break;
+            }
         }
-        if (fit >= want_rows) break;
     }
     if (best_rows < 16) return false;
     L = best;
