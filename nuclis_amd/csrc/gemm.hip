@@ -530,6 +530,12 @@ __device__ __forceinline__ void tile_coords(uint32_t id, uint32_t tm, uint32_t t
 // NW = 4: 2 x 2 waves of 128 x 128, 256 accumulators per lane (each thread
 // stages a whole weight row). The larger wave tile halves the LDS fragment
 // reads per MFMA.
+// Instruction groups of the K step (sched_group_barrier): MFMA 1, LDS read 1,
+// VALU PF_SCHED_VALU, repeated. Left to itself the scheduler bunched the
+// MFMAs and the dequantisation apart; interleaved, Q4_K 17408 x 5120 went
+// from ~815 to ~845 TFLOP/s at 4096 tokens and 532 to 555 at 512 on MI355X
+// (4, 12, 16 and 20 were no better; Q6_K is unchanged).
+constexpr int PF_SCHED_VALU = 8;
 template <uint32_t ENC, typename XT, uint32_t NW>
 __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                               uint32_t rows, uint32_t columns,
@@ -658,6 +664,13 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
             /* the last step dequantises into the idle buffer; harmless */                                         \
             _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_)                                                 \
                 WNEXT[s_].dequant(ks_ + 1, NUQ_PF_PART(s_), kk, wdst);                                             \
+            /* scheduling: each MFMA, then one fragment read, then up to PF_SCHED_VALU */                        \
+            /* dequantisation VALU ops, so they issue under the MFMA's 32 cycles */                                  \
+            _Pragma("unroll") for (int q_ = 0; q_ < 4 * (int)TJ; ++q_) {                                           \
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                 \
+                __builtin_amdgcn_sched_group_barrier(0x002, PF_SCHED_VALU, 0);                                     \
+            }                                                                                                      \
         }                                                                                                          \
         if (!DMA && next) {                                                                                        \
             _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) {                                               \
