@@ -275,6 +275,34 @@ struct XLoad<float> {
     }
 };
 
+typedef _Float16 half4v_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two f16 values 1024 + v from bytes i and j of t (each v < 1024): the
+// byte goes into the low mantissa byte of 1024.0 (0x6400, ulp 1) by one
+// v_perm_b32 whose second source supplies the 0x64 exponent bytes.
+template <int I, int J>
+__device__ __forceinline__ half2v f16_biased(uint32_t t) {
+    constexpr uint32_t sel = (uint32_t)I | (4u << 8) | ((uint32_t)J << 16) | (4u << 24);
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, t, sel));
+}
+
+// Four weights mul*(b - bias) + add, rounded to f16, from the four bytes b of
+// t: the bytes become exact f16 integers b - bias (one v_perm_b32 and one
+// v_pk_add_f16 per pair), and the F32 product-sum is rounded to f16 by
+// v_fma_mix (the F32 FMA's value, converted).
+__device__ __forceinline__ half4v_t pf_four(uint32_t t, _Float16 bias, float mul, float add) {
+    const half2v p = f16_biased<0, 1>(t) - (half2v){bias, bias};
+    const half2v q = f16_biased<2, 3>(t) - (half2v){bias, bias};
+    half4v_t r;
+    r[0] = (_Float16)fmaf((float)p[0], mul, add);
+    r[1] = (_Float16)fmaf((float)p[1], mul, add);
+    r[2] = (_Float16)fmaf((float)q[0], mul, add);
+    r[3] = (_Float16)fmaf((float)q[1], mul, add);
+    return r;
+}
+
 // Raw bytes of the 32 weight values a thread owns in one K slab, kept in
 // registers between the global load and the dequantisation. `dequant(c)`
 // writes chunk c (0..3) of the 32 values, so the work can be spread between
@@ -307,18 +335,8 @@ struct WRaw<12> {
         }
         const uint32_t word = c == 0 ? qs.x : c == 1 ? qs.y : c == 2 ? qs.z : qs.w;
         const uint32_t lo = opaque_and<0x0f0f0f0fu>(word), hi = opaque_and<0xf0f0f0f0u>(word);
-        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-        half4 l, h;
-        l[0] = (_Float16)fmaf(mul0, ubyte_f<0>(lo), -off0);
-        l[1] = (_Float16)fmaf(mul0, ubyte_f<1>(lo), -off0);
-        l[2] = (_Float16)fmaf(mul0, ubyte_f<2>(lo), -off0);
-        l[3] = (_Float16)fmaf(mul0, ubyte_f<3>(lo), -off0);
-        h[0] = (_Float16)fmaf(mul1, ubyte_f<0>(hi), -off1);
-        h[1] = (_Float16)fmaf(mul1, ubyte_f<1>(hi), -off1);
-        h[2] = (_Float16)fmaf(mul1, ubyte_f<2>(hi), -off1);
-        h[3] = (_Float16)fmaf(mul1, ubyte_f<3>(hi), -off1);
-        *(half4 *)(out + part * 16 + 4 * c) = l;
-        *(half4 *)(out + 32 + part * 16 + 4 * c) = h;
+        *(half4v_t *)(out + part * 16 + 4 * c) = pf_four(lo, (_Float16)1024.f, mul0, -off0);
+        *(half4v_t *)(out + 32 + part * 16 + 4 * c) = pf_four(hi, (_Float16)1024.f, mul1, -off1);
     }
 };
 template <>
@@ -354,10 +372,13 @@ struct WRaw<14> {
         for (int kk = 0; kk < 2; ++kk) {
             const uint32_t u = opaque_and<0x0f0f0f0fu>(ql[2 * c + kk] >> lshift) |
                                opaque_and<0x30303030u>((qh[2 * c + kk] >> hshift) << 4);
-            v[kk * 4 + 0] = (_Float16)fmaf(mul, ubyte_f<0>(u), -32.f * mul);
-            v[kk * 4 + 1] = (_Float16)fmaf(mul, ubyte_f<1>(u), -32.f * mul);
-            v[kk * 4 + 2] = (_Float16)fmaf(mul, ubyte_f<2>(u), -32.f * mul);
-            v[kk * 4 + 3] = (_Float16)fmaf(mul, ubyte_f<3>(u), -32.f * mul);
+            // mul * (q - 32): the product of the exact f16 integer q - 32
+            // equals the former fma(mul, q, -32 * mul) before rounding
+            const half4v_t f = pf_four(u, (_Float16)1056.f, mul, 0.f);
+            v[kk * 4 + 0] = f[0];
+            v[kk * 4 + 1] = f[1];
+            v[kk * 4 + 2] = f[2];
+            v[kk * 4 + 3] = f[3];
         }
         *(half8 *)(out + part * 32 + 8 * c) = v;
     }
@@ -996,17 +1017,6 @@ struct VLane<8> {
     }
 };
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Two f16 values 1024 + v from bytes i and j of t (each v < 1024): the
-// byte goes into the low mantissa byte of 1024.0 (0x6400, ulp 1) by one
-// v_perm_b32 whose second source supplies the 0x64 exponent bytes.
-template <int I, int J>
-__device__ __forceinline__ half2v f16_biased(uint32_t t) {
-    constexpr uint32_t sel = (uint32_t)I | (4u << 8) | ((uint32_t)J << 16) | (4u << 24);
-    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, t, sel));
-}
 
 // Two f16 values 1024 + (t & M) from the halves of t (M keeps at most bits
 // 0-9 of each half): (t & M) | 0x64006400 as one v_and_or_b32.
