@@ -302,8 +302,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is design-only "
-                                   "(rows split across GPUs, see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; sharding across GPUs "
+                                   "(each GPU holding whole weight rows) is not built", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
 
