@@ -407,11 +407,13 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
     args.mode = mode;
     const uint32_t rpw = (uint32_t)nuq::segment_rows_per_wave();
     uint32_t waves = 0;
+    uint64_t strides[4];
     for (uint32_t i = 0; i < count; ++i) {
         const nuq_matrix &m = segments[i].matrix;
         uint64_t stride;
         int e = check_matrix(ctx, &m, &stride);
         if (e) return e;
+        strides[i] = stride;
         if (m.rows % 16 != 0 || m.columns != columns)
             return fail(ctx, NUQ_INVALID_SHAPE, "segment %u: rows %% 16 and equal columns required", i);
         if (!segments[i].output || (uintptr_t)segments[i].output % 4 != 0)
@@ -436,11 +438,38 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
         waves += (uint32_t)((m.rows + rpw - 1) / rpw);
     }
     args.wave_start[count] = waves;
-    // A large SiLU pair streams faster as two decode GEMVs (gate into the
-    // output, up into the prefill workspace, which no GEMV uses) and the
-    // elementwise epilogue than as one merged row-per-wave pass.
-    if (mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only && segments[0].matrix.rows >= PAIR_SPLIT_ROWS &&
-        segments[0].matrix.rows * sizeof(float) <= (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float)) {
+    // A large SiLU pair streams faster as decode GEMVs (gate into the output,
+    // up into the prefill workspace, which no GEMV uses) and the elementwise
+    // epilogue than as one merged row-per-wave pass.
+    const bool pair_split = mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only &&
+                            segments[0].matrix.rows >= PAIR_SPLIT_ROWS &&
+                            segments[0].matrix.rows * sizeof(float) <=
+                                (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float);
+    // Segments of one encoding and row stride (q/k/v, gate/up) run as one
+    // launch of the decode GEMV, each matrix on its share of the workgroups.
+    bool same = !ctx->generic_only && (mode == NUQ_SEGMENT_PLAIN || pair_split);
+    for (uint32_t i = 1; i < count && same; ++i)
+        same = segments[i].matrix.encoding == segments[0].matrix.encoding && strides[i] == strides[0];
+    if (same) {
+        const uint8_t *ws[4];
+        uint32_t rs[4];
+        float *ys[4];
+        for (uint32_t i = 0; i < count; ++i) {
+            ws[i] = (const uint8_t *)segments[i].matrix.bytes;
+            rs[i] = (uint32_t)segments[i].matrix.rows;
+            ys[i] = segments[i].output;
+        }
+        if (mode != NUQ_SEGMENT_PLAIN) ys[1] = ctx->split.work;
+        const hipError_t he = nuq::launch_gemv_dma_segments(ctx->stream, segments[0].matrix.encoding, count, ws,
+                                                            strides[0], rs, (uint32_t)columns, x, ys);
+        if (he != hipErrorInvalidValue) {
+            int e = hip_check(ctx, he, "segments gemv launch");
+            if (e || mode == NUQ_SEGMENT_PLAIN) return e;
+            return hip_check(ctx, nuq::launch_silu_mul(ctx->stream, segments[0].output, ctx->split.work, rs[0]),
+                             "silu pair epilogue");
+        }
+    }
+    if (pair_split) {
         const nuq_matrix &g = segments[0].matrix, &u = segments[1].matrix;
         float *up = ctx->split.work;
         int e = run_gemv(ctx, &g, g.byte_len / g.rows, x, segments[0].output);

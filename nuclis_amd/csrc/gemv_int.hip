@@ -707,8 +707,27 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
                                                                       const float *__restrict__ x,
-                                                                      float *__restrict__ y, uint32_t tail) {
+                                                                      float *__restrict__ y, uint32_t tail,
+                                                                      GdSegments segs) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    // Segments: workgroups [wg_end[q-1], wg_end[q]) run matrix q. Each entry
+    // is read with a constant index, so the table stays in scalar registers.
+    uint32_t blk = blockIdx.x;
+    if (segs.count) {
+        w = segs.w[0];
+        y = segs.y[0];
+        rows = segs.rows[0];
+        rows_per_wg = segs.rows_per_wg[0];
+#pragma unroll
+        for (uint32_t q = 1; q < GD_MAX_SEGMENTS; ++q)
+            if (q < segs.count && blockIdx.x >= segs.wg_end[q - 1]) {
+                w = segs.w[q];
+                y = segs.y[q];
+                rows = segs.rows[q];
+                rows_per_wg = segs.rows_per_wg[q];
+                blk = blockIdx.x - segs.wg_end[q - 1];
+            }
+    }
     if (tail && blockIdx.x == gridDim.x - 1) {
         // The matrix's last row (rows is the count without it), when a row
         // ends mid-chunk: its last copy would read past the weights, so this
@@ -747,7 +766,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
     static_assert(GROUPS * ROW_CHUNKS == BYTES && SLOTS * BYTES % 16 == 0, "one step is BYTES chunks");
     const bool direct = j < 2;
     const uint32_t shift = direct ? 16 * j : 16 * j - 32;
-    const uint32_t row_begin = blockIdx.x * rows_per_wg;
+    const uint32_t row_begin = blk * rows_per_wg;
     const uint32_t row_end = min(row_begin + rows_per_wg, rows);
     const uint32_t b = SLOTS * kw + slot;
     const bool live = b < nblocks;
@@ -903,7 +922,53 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
     hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)),
                        dim3(64 * waves), lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y,
-                       tail ? 1u : 0u);
+                       tail ? 1u : 0u, GdSegments{});
+    return hipGetLastError();
+}
+
+// Several matrices of one encoding and row stride against one x in a single
+// launch: each gets whole workgroups, in proportion to its rows (at least
+// one), and streams as it would alone. A row's sum does not depend on the
+// workgroup split, so each output equals the matrix's own GEMV bit for bit.
+template <uint32_t ENC, int SLOTS, int D>
+static hipError_t launch_dma_segments(hipStream_t s, uint32_t count, const uint8_t *const *w, uint64_t stride,
+                                      const uint32_t *rows, uint32_t nblocks, const float *x, float *const *y) {
+    if (count == 0 || count > GD_MAX_SEGMENTS) return hipErrorInvalidValue;
+    constexpr uint32_t cus = 256;
+    uint64_t total = 0;
+    for (uint32_t q = 0; q < count; ++q) {
+        if (rows[q] == 0) return hipErrorInvalidValue;
+        total += rows[q];
+    }
+    GdSegments segs{};
+    segs.count = count;
+    uint32_t wgs = 0, max_rpw = 0;
+    for (uint32_t q = 0; q < count; ++q) {
+        const uint32_t share = std::max<uint32_t>(1, (uint32_t)((cus * (uint64_t)rows[q] + total / 2) / total));
+        const uint32_t rpw = (rows[q] + share - 1) / share;
+        if ((uint64_t)rpw * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
+        segs.w[q] = w[q];
+        segs.y[q] = y[q];
+        segs.rows[q] = rows[q];
+        segs.rows_per_wg[q] = rpw;
+        wgs += (rows[q] + rpw - 1) / rpw;
+        segs.wg_end[q] = wgs;
+        max_rpw = std::max(max_rpw, rpw);
+    }
+    const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
+    const uint32_t step_rows = 64 / (4 * SLOTS);
+    uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
+    sets = std::min(sets, std::max(1u, (uint32_t)(total / (cus * step_rows))));
+    auto lds_for = [&](uint32_t st) {
+        const size_t wv = (size_t)set_waves * st;
+        return wv * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
+               ((size_t)max_rpw * set_waves + wv) * 4;
+    };
+    while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
+    const size_t lds = lds_for(sets);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3(wgs), dim3(64 * set_waves * sets), lds, s, w[0], stride,
+                       rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
     return hipGetLastError();
 }
 
@@ -994,6 +1059,27 @@ hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, u
     if (encoding == 23 && nblocks % 2 == 0)
         return four ? launch_dma<23, 4, 2>(s, w, stride, rows, nblocks, x, y, 0, 1)
                     : launch_dma<23, 8, 2>(s, w, stride, rows, nblocks, x, y, 0, 1);
+    return hipErrorInvalidValue;
+}
+
+// The segment form of the DMA GEMV for every encoding launch_gemv_dma and
+// the Q4_K DMA path take, when no row needs the separate last-row workgroup.
+hipError_t launch_gemv_dma_segments(hipStream_t s, uint32_t encoding, uint32_t count, const uint8_t *const *w,
+                                    uint64_t stride, const uint32_t *rows, uint32_t columns, const float *x,
+                                    float *const *y) {
+    const uint32_t nblocks = columns / 256;
+    if (columns % 256 != 0 || cdiv(nblocks, 8) > GI_MAX_SET_WAVES) return hipErrorInvalidValue;
+    const bool four = cdiv(nblocks, 4) <= GI_MAX_SET_WAVES;
+#define NUQ_GD_SEG(E_) \
+    return four ? launch_dma_segments<E_, 4, 2>(s, count, w, stride, rows, nblocks, x, y) \
+                : launch_dma_segments<E_, 8, 2>(s, count, w, stride, rows, nblocks, x, y);
+    if (encoding == 12) NUQ_GD_SEG(12)
+    if (encoding == 13) NUQ_GD_SEG(13)
+    if (encoding == 8) NUQ_GD_SEG(8)
+    if (encoding == 23 && nblocks % 2 == 0) NUQ_GD_SEG(23)
+#undef NUQ_GD_SEG
+    if (encoding == 14 && nblocks * 210u % 16 == 0)
+        return launch_dma_segments<14, 8, 2>(s, count, w, stride, rows, nblocks, x, y);
     return hipErrorInvalidValue;
 }
 

@@ -36,6 +36,21 @@ hipError_t launch_gemv(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const float *x, float *y, int rows_per_wave);
 hipError_t launch_gemv_q4k_int(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                const float *x, float *y, int config);
+// Up to GD_MAX_SEGMENTS matrices of one encoding and row stride against one
+// x in one DMA GEMV launch (y[q] = W_q x). hipErrorInvalidValue when the
+// shape does not fit it.
+constexpr uint32_t GD_MAX_SEGMENTS = 4;
+struct GdSegments {
+    const uint8_t *w[GD_MAX_SEGMENTS];
+    float *y[GD_MAX_SEGMENTS];
+    uint32_t rows[GD_MAX_SEGMENTS];
+    uint32_t rows_per_wg[GD_MAX_SEGMENTS];
+    uint32_t wg_end[GD_MAX_SEGMENTS];
+    uint32_t count;  // 0: one matrix, from the kernel's own arguments
+};
+hipError_t launch_gemv_dma_segments(hipStream_t s, uint32_t encoding, uint32_t count, const uint8_t *const *w,
+                                    uint64_t stride, const uint32_t *rows, uint32_t columns, const float *x,
+                                    float *const *y);
 hipError_t launch_gemv_dma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                            uint32_t columns, const float *x, float *y);
 hipError_t launch_generic(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,

@@ -448,6 +448,38 @@ def test_silu_pair_large_runs_as_two_gemvs(backend, rows):
     assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
 
 
+@pytest.mark.parametrize("encoding,columns,rows", [
+    (12, 5120, (6144, 1024, 1024)),   # config-3 q/k/v
+    (12, 5120, (17408,)),
+    (12, 17408, (512, 16, 1040, 2048)),
+    (13, 5120, (1024, 48)),
+    (14, 8192, (512, 256)),
+    (8, 4096, (4096, 1024, 32)),
+    (23, 5120, (2048, 1024, 16)),
+])
+def test_segments_one_encoding_run_as_one_gemv(backend, encoding, columns, rows):
+    """Segments of one encoding and row stride run as one launch of the decode
+    GEMV: every output equals the matrix's own matvec bit for bit (the same
+    per-row arithmetic), and stays within the integer-dot bound of the oracle."""
+    import torch
+    ws = [quantized(encoding, r, columns, 70 + i) for i, r in enumerate(rows)]
+    x = gaussian(71, columns)
+    xg = to_gpu(x)
+    mats = [nq.Matrix(encoding, r, columns, to_gpu(w)) for r, w in zip(rows, ws)]
+    outs = [torch.full((r,), np.nan, device="cuda") for r in rows]
+    singles = [torch.full((r,), np.nan, device="cuda") for r in rows]
+    backend.matvec_segments(list(zip(mats, outs)), xg, nq.SEGMENT_PLAIN)
+    for m, o in zip(mats, singles):
+        backend.matvec(m, xg, o)
+    backend.sync()
+    for r, w, o, one in zip(rows, ws, outs, singles):
+        got = o.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), one.cpu().numpy().view(np.uint32))
+        want = orc.matvec(encoding, r, columns, w, x).astype(np.float64)
+        bound = F32_K * mass(encoding, w, r, columns, x)[0] + xq_mass(encoding, w, r, columns, x)[0] + 1e-6
+        assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
+
+
 def segments_plain(backend, shapes):
     import torch
     columns = 5120
