@@ -1778,9 +1778,6 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // holds at least 16 rows (the kernel's steps assume it). Ranges differ by
     // at most one row.
     const uint32_t want_rows = std::max(16u, (rows * ranges + 255) / 256);
-    // Candidates in order of preference: private staging, shared staging,
-    // direct loads (the only one for F32 activations); the first whose rings
-    // and partial sums hold want_rows rows, else the one holding the most.
     // Candidates in order of preference: three ring slots (two steps in
     // flight while one computes), then two; within each, private staging,
     // shared staging, direct loads (the only one for F32 activations). The
