@@ -480,9 +480,16 @@ def test_segments_one_encoding_run_as_one_gemv(backend, encoding, columns, rows)
         assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
 
 
+def test_segments_fall_back_when_the_gemv_does_not_fit(backend):
+    """At K = 32768 the decode GEMV's x slices and rings exceed the LDS, so
+    one-encoding segments run on the merged row kernel (F32 bound)."""
+    segments_plain(backend, [(12, 64, 32768), (12, 32, 32768)])
+
+
 def segments_plain(backend, shapes):
     import torch
-    columns = 5120
+    columns = shapes[0][2] if len(shapes[0]) > 2 else 5120
+    shapes = [s_[:2] for s_ in shapes]
     ws = [quantized(e, r, columns, 40 + i) for i, (e, r) in enumerate(shapes)]
     x = gaussian(41, columns)
     xg = to_gpu(x)
