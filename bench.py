@@ -4,12 +4,19 @@ Headline: Q4_K GEMV GB/s (% of HBM peak) at 5120 -> 17408,
 M=1 (configs[1], gate/up shape), plus the prefill GEMM TFLOP/s at M=4096.
 
 A "step" is one Q4_K GEMV over one weight copy: y = W x, W 17408 x 5120 Q4_K
-(50,135,040 B), x F32 5120. Inputs are resident in HBM. The timed region
-replays a HIP graph of back-to-back GEMVs that rotate over enough distinct
-weight copies (>= 512 MB) that every call streams from HBM and not from the
-256 MB Infinity Cache. `value` = weight bytes per step x steps / wall time;
-the roofline uses the algorithmic bytes (weights + x + y) over the average
-launch duration measured with HIP events on the launch stream.
+(50,135,040 B), x F32 5120. Inputs are resident in HBM. The timed region is
+one replay of a HIP graph of exactly --steps back-to-back GEMVs that rotate
+over enough distinct weight copies (>= 512 MB) that every call streams from
+HBM and not from the 256 MB Infinity Cache, after --warmup launches of the
+same rotation. `value` = weight bytes x steps / the region's duration, from
+HIP events on the launch stream; the roofline uses the algorithmic bytes
+(weights + x + y) per launch over the same average launch duration.
+
+Every other configuration runs by default with its own fixed repetition
+count (configs[0], the configs[1] down shape, the configs[2] layer step
+with its greedy token, configs[3] M=8 verify on both kernels, configs[4]
+prefill at M=512 and M=4096 on both matrices), each output checked against
+the CPU oracle (a row or token sample) before it is reported.
 
 cpu_baseline: the CPU oracle's matvec (the C restatement of nuclis's
 cpu.matvec; the Zig reference cannot be built here) on the same matrix, timed
@@ -34,6 +41,9 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
 MALL_BYTES = 256 << 20
+GEMV_KERNEL = "gemv_dma_kernel<12, 4, 2>"
+GEMV_DTYPE = ("q4_k codes x f32 activations rounded to 16-bit fixed point per 32-value slice "
+              "(int8 byte planes, exact int32 dot) -> f32 scale/accumulate")
 
 
 def parse():
@@ -41,10 +51,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2000)
     p.add_argument("--warmup", type=int, default=200)
-    p.add_argument("--extras", action="store_true", help="also time the other configs (verify, layer, Q6_K)")
+    p.add_argument("--extras", action="store_true",
+                   help="also time the lm_head GEMV, Q5_K / IQ4_XS, GGUF upload and sampling")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", default="", help="comma list: gemv,prefill")
+    p.add_argument("--only", default="", help="comma list of: configs, prefill (the headline GEMV always runs)")
     p.add_argument("--profile-copy", action="store_true",
                    help="also run one plain 256 MiB device copy (the calibration kernel for rocprofv3 byte counters)")
     return p.parse_args()
@@ -148,10 +159,17 @@ def copies_for(nbytes: int) -> int:
     return max(8, -(-2 * MALL_BYTES // nbytes))
 
 
-def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmup, seed=2):
+def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmup, w_seed, x_seed=1):
+    """`steps` decode GEMVs timed as one replay of a HIP graph of exactly
+    `steps` launches, rotating over `copies` distinct weight copies (>= 512
+    MB) so each launch streams from HBM rather than the 256 MB Infinity
+    Cache; `warmup` launches of the same rotation replay untimed first. The
+    timed region is bracketed by synchronizations and HIP events on the
+    launch stream."""
     from nuclis_amd.synth import gaussian
-    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
-    x = torch.from_numpy(gaussian(1, columns)).cuda()
+    steps, warmup = max(1, steps), max(0, warmup)
+    w = nq.quantize(encoding, gaussian(w_seed, (rows, columns), 0.02))
+    x = torch.from_numpy(gaussian(x_seed, columns)).cuda()
     ncopies = copies_for(w.nbytes)
     base = torch.from_numpy(w).cuda()
     mats = [nq.Matrix(encoding, rows, columns, base if i == 0 else base.clone()) for i in range(ncopies)]
@@ -161,51 +179,75 @@ def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmu
         for i in range(ncopies):
             backend.matvec(mats[i], x, ys[i])
         eager = [y.clone() for y in ys]
-        # one graph = one pass over every copy
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(ncopies):
-                backend.matvec(mats[i], x, ys[i])
-        reps = max(1, steps // ncopies)
-        wreps = max(1, warmup // ncopies)
-        for _ in range(wreps):
-            graph.replay()
-        torch.cuda.synchronize()
-        for i in range(ncopies):  # every replay must equal the eager result
-            assert torch.equal(ys[i], eager[i]), "graph replay differs from eager GEMV"
+
+        def capture(n):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(n):
+                    backend.matvec(mats[i % ncopies], x, ys[i % ncopies])
+            return graph
+        timed = capture(steps)
+        if warmup:
+            capture(warmup).replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         with Timer(torch, stream) as t:
-            for _ in range(reps):
-                graph.replay()
+            timed.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    launches = reps * ncopies
+        for i in range(min(steps, ncopies)):  # every replay must equal the eager result
+            assert torch.equal(ys[i], eager[i]), "graph replay differs from the eager GEMV"
     weight_bytes = w.nbytes
     algo_bytes = weight_bytes + columns * 4 + rows * 4
-    kernel_s = t.ms / 1e3 / launches
+    kernel_s = t.ms / 1e3 / steps
     return {
-        "launches": launches, "copies": ncopies, "wall_s": wall, "event_ms": t.ms,
+        "launches": steps, "warmup_launches": warmup, "copies": ncopies, "wall_s": wall, "event_ms": t.ms,
         "weight_bytes": weight_bytes, "algo_bytes": algo_bytes,
         "us_per_launch": kernel_s * 1e6,
         "weight_gbs": weight_bytes / kernel_s / 1e9,
         "algo_gbs": algo_bytes / kernel_s / 1e9,
-        "wall_weight_gbs": weight_bytes * launches / wall / 1e9,
+        "wall_weight_gbs": weight_bytes * steps / wall / 1e9,
         "w": w, "x": x, "y0": eager[0],
     }
 
 
-def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps=20, warmup=3, seed=2,
-               kernel=None):
+def public(d):
+    return {k: v for k, v in d.items() if k not in ("w", "x", "y0", "out", "xh")}
+
+
+def check_gemv(orc, g, encoding, rows, columns, stride_rows=97):
+    """The timed GEMV's output against the oracle on every stride_rows-th row:
+    the F32 bound |d| <= 4e-6 * sum|w*x| + 1e-6 plus the activation rounding
+    term of the integer-dot kernel, and the normwise 2e-3."""
+    x_host = g["x"].cpu().numpy()
+    sample = np.arange(0, rows, stride_rows)
+    w = np.ascontiguousarray(g["w"][sample])
+    ref = orc.matvec(encoding, sample.size, columns, w, x_host).astype(np.float64)
+    got = g["y0"].cpu().numpy()[sample].astype(np.float64)
+    dec = np.abs(orc.decode_matrix(encoding, w, sample.size, columns).astype(np.float64))
+    m = dec @ np.abs(x_host.astype(np.float64))
+    amax = np.repeat(np.abs(x_host.astype(np.float64)).reshape(-1, 32).max(-1), 32)
+    bound = 4e-6 * m + dec @ (amax / 65278.0) + 1e-6
+    err = np.abs(got - ref)
+    assert np.all(err <= bound), f"GEMV enc {encoding} {rows}x{columns} outside the bound"
+    return {"rows_checked": int(sample.size), "normwise": float(err.max() / np.abs(ref).max()),
+            "worst_err_over_mass": float((err / m).max())}
+
+
+def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps=20, warmup=3, w_seed=2,
+               x_seed=5, kernel=None, check=None):
+    """`reps` launches of the matmul entry point (one kernel route) on
+    rotating weight copies (>= 512 MB), f16 activations; HIP events on the
+    launch stream. `check` = (orc, token sample): the timed output is
+    compared with the oracle on every row of those tokens."""
     from nuclis_amd.synth import gaussian
-    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
-    x = torch.from_numpy(gaussian(7, (tokens, columns))).cuda().to(torch.float16)
+    w = nq.quantize(encoding, gaussian(w_seed, (rows, columns), 0.02))
+    xh = gaussian(x_seed, (tokens, columns)).astype(np.float16)
+    x = torch.from_numpy(xh).cuda()
     wg = torch.from_numpy(w).cuda()
-    # rotating weight copies (>= 512 MB), so every launch streams from HBM
-    # and not from the 256 MB last-level cache
     mats = [nq.Matrix(encoding, rows, columns, wg if i == 0 else wg.clone()) for i in range(copies_for(w.nbytes))]
-    y = torch.empty((tokens, rows), device="cuda")
-    k = nq.KERNEL_TILE if kernel is None else kernel
+    y = torch.full((tokens, rows), float("nan"), device="cuda")
+    k = nq.KERNEL_AUTO if kernel is None else kernel
     stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         for i in range(warmup):
@@ -214,10 +256,30 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
         with Timer(torch, stream) as t:
             for i in range(reps):
                 backend.matmul_kernel(k, mats[i % len(mats)], x, columns, y, rows, tokens)
+        torch.cuda.synchronize()
     s = t.ms / 1e3 / reps
     flops = 2.0 * tokens * rows * columns
-    return {"ms": s * 1e3, "tflops": flops / s / 1e12, "flops": flops, "weight_gbs": w.nbytes / s / 1e9,
-            "frac_f16_peak": flops / s / 1e12 / F16_PEAK_TFLOPS}
+    out = {"ms": s * 1e3, "tflops": flops / s / 1e12, "flops": flops, "weight_gbs": w.nbytes / s / 1e9,
+           "frac_f16_peak": flops / s / 1e12 / F16_PEAK_TFLOPS, "reps": reps}
+    if check is not None:
+        orc, sel, kbound = check
+        got = y.cpu().numpy()[sel].astype(np.float64)
+        xr = xh[sel].astype(np.float32)
+        ref = orc.matmul(encoding, rows, columns, w, xr).astype(np.float64)
+        dec = np.abs(orc.decode_matrix(encoding, w, rows, columns).astype(np.float64))
+        m = np.abs(xr.astype(np.float64)) @ dec.T
+        err = np.abs(got - ref)
+        assert np.all(err <= kbound * m + 1e-6), f"matmul enc {encoding} {rows}x{columns} M={tokens} outside the bound"
+        out["check"] = {"tokens_checked": int(len(sel)), "rows_checked": rows, "bound": f"{kbound:g}*sum|w*x|+1e-6",
+                        "worst_err_over_mass": float((err / m).max()),
+                        "normwise": float(err.max() / np.abs(ref).max())}
+    return out
+
+
+def token_sample(tokens):
+    """First and last token of every 256-token tile (every output tile)."""
+    t = sorted({s for start in range(0, tokens, 256) for s in (start, min(start + 255, tokens - 1))})
+    return np.array(t)
 
 
 def bench_library_gemm(torch, stream, rows, columns, tokens, reps=20, warmup=3):
@@ -240,14 +302,17 @@ def bench_library_gemm(torch, stream, rows, columns, tokens, reps=20, warmup=3):
     return {"ms": s * 1e3, "tflops": 2.0 * tokens * rows * columns / s / 1e12}
 
 
-def bench_layer(torch, nq, backend, stream, reps=20):
+def bench_layer(torch, nq, backend, stream, reps=20, check=None):
     """Configuration 3: one decode step (q/k/v, o, gate/up, down Q4_K + Q6_K
-    lm_head, M=1) captured as a HIP graph; GB/s of weight bytes per step."""
+    lm_head, M=1) captured as a HIP graph; GB/s of weight bytes per step.
+    `check` = the oracle module: the greedy token must equal the CPU
+    composition's."""
     from nuclis_amd import layer as L
     from nuclis_amd.synth import gaussian
     weights = L.quantized_weights()
     dev = L.upload(weights)
-    x = torch.from_numpy(gaussian(20, L.HIDDEN)).cuda()
+    xh = gaussian(20, L.HIDDEN)
+    x = torch.from_numpy(xh).cuda()
     stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         L.step(backend, dev, x)
@@ -265,12 +330,26 @@ def bench_layer(torch, nq, backend, stream, reps=20):
         token = backend.argmax(dev.buffers["logits"])
     s = t.ms / 1e3 / reps
     nbytes = L.weight_bytes(weights)
-    return {"us_per_step": s * 1e6, "weight_bytes": nbytes, "weight_gbs": nbytes / s / 1e9, "token": token}
+    out = {"us_per_step": s * 1e6, "weight_bytes": nbytes, "weight_gbs": nbytes / s / 1e9, "token": token,
+           "reps": reps}
+    if check is not None:
+        from oracle import layer_oracle
+        ref = layer_oracle.cpu_step(L.SHAPES, weights, xh)
+        want = check.argmax(ref)
+        assert token == want, f"layer step greedy token {token} != oracle {want}"
+        out["oracle_token"] = want
+    del dev
+    return out
+
+
+TRAFFIC_PROFILE = "gemv_q4k_17408x5120_traffic"
 
 
 def measured_traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
-    copy-kernel calibrated) and recorded in profiles/<name>.md; None if absent."""
+    """HBM bytes per launch from a rocprofv3 --pmc run (FETCH_SIZE +
+    WRITE_SIZE, copy-kernel calibrated) recorded in profiles/<name>.md; None
+    if absent. Counters cannot be read inside this process, so this figure is
+    the profiled run's, not this run's."""
     path = ROOT / "profiles" / f"{name}.md"
     if not path.exists():
         return None
@@ -308,6 +387,8 @@ def main():
     import torch
 
     import nuclis_amd as nq
+    from nuclis_amd.synth import CONFIGS
+    from oracle import oracle as orc
     torch.cuda.init()
     backend = nq.Backend(0)
     stream = torch.cuda.Stream()
@@ -318,75 +399,87 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    rows, columns = 17408, 5120
-    out = {}
-    g = bench_gemv(torch, nq, backend, stream, nq.Q4_K, rows, columns, args.steps, args.warmup)
-    # correctness of the timed kernel against the oracle on a row sample
-    from oracle import oracle as orc
-    x_host = g["x"].cpu().numpy()
-    sample = np.arange(0, rows, 97)
-    ref = orc.matvec(12, sample.size, columns, np.ascontiguousarray(g["w"][sample]), x_host)
-    got = g["y0"].cpu().numpy()[sample]
-    normwise = float(np.abs(got - ref).max() / np.abs(ref).max())
-    assert normwise <= 2e-3, normwise
+
+    def want(name):
+        return not only or name in only
+
+    # headline: configs[1] gate/up GEMV, exactly --steps launches timed
+    enc, rows, columns, seed = CONFIGS["c2_gate"]
+    g = bench_gemv(torch, nq, backend, stream, enc, rows, columns, args.steps, args.warmup, seed)
+    gcheck = check_gemv(orc, g, enc, rows, columns)
+    configs = {}
+    fixed = 200  # launches per secondary GEMV line, whatever --steps is
+    if want("configs"):
+        for key, name in (("configs[0] q8_0 4096x4096", "c1_q8_0"), ("configs[1] q4_k down 5120x17408", "c2_down")):
+            e, r, c, sd = CONFIGS[name]
+            d = bench_gemv(torch, nq, backend, stream, e, r, c, fixed, 50, sd)
+            d["check"] = check_gemv(orc, d, e, r, c)
+            d["roofline_frac"] = d["algo_gbs"] / HBM_PEAK_GBS
+            configs[key] = public(d)
+        configs["configs[2] layer step + q6_k lm_head"] = bench_layer(torch, nq, backend, stream, check=orc)
+        e, r, c, sd = CONFIGS["c2_gate"]
+        e2, r2, c2, sd2 = CONFIGS["c2_down"]
+        for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
+            for label, (ee, rr, cc, ss) in (("gate 17408x5120", (e, r, c, sd)), ("down 5120x17408", (e2, r2, c2, sd2))):
+                d = bench_gemm(torch, nq, backend, stream, ee, rr, cc, 8, reps=200, warmup=20, w_seed=ss, x_seed=4,
+                               kernel=kid, check=(orc, np.arange(8), 4e-6 if kname == "rows" else 2e-4))
+                d["algo_gbs"] = (rr * cc // 256 * 144 + 8 * cc * 2 + 8 * rr * 4) / d["ms"] / 1e6
+                configs[f"configs[3] verify M=8 q4_k {label} {kname}"] = d
     prefill = None
-    if not only or "prefill" in only:
-        prefill = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 4096)
-        prefill["library"] = bench_library_gemm(torch, stream, 17408, 5120, 4096)
+    if want("prefill"):
+        e, r, c, sd = CONFIGS["c5_gate"]
+        prefill = bench_gemm(torch, nq, backend, stream, e, r, c, 4096, w_seed=sd,
+                             check=(orc, token_sample(4096), 2e-4))
+        prefill["library"] = bench_library_gemm(torch, stream, r, c, 4096)
+        if want("configs"):
+            for label, name, tokens in (("q4_k gate 17408x5120 M=512", "c5_gate", 512),
+                                        ("q6_k down 5120x17408 M=4096", "c5_down", 4096),
+                                        ("q6_k down 5120x17408 M=512", "c5_down", 512)):
+                e, r, c, sd = CONFIGS[name]
+                configs[f"configs[4] prefill {label}"] = bench_gemm(torch, nq, backend, stream, e, r, c, tokens,
+                                                                    w_seed=sd, check=(orc, token_sample(tokens), 2e-4))
     extras = {}
     if args.extras:
-        extras["q4k_down_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q4_K, 5120, 17408,
-                                                                 args.steps, args.warmup).items()
-                                   if k not in ("w", "x", "y0")}
-        extras["q6k_lmhead_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q6_K, 151936, 5120,
-                                                                   64, 8).items() if k not in ("w", "x", "y0")}
-        extras["decode_layer_step"] = bench_layer(torch, nq, backend, stream)
+        extras["q6k_lmhead_gemv"] = public(bench_gemv(torch, nq, backend, stream, nq.Q6_K, 151936, 5120, 64, 8, 17))
         extras["gguf_upload"] = bench_upload(torch, nq, backend)
         extras["sampling"] = bench_sampling(torch, nq, backend, stream)
-        extras["q8_0_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, nq.Q8_0, 4096, 4096,
-                                                             args.steps, args.warmup).items()
-                               if k not in ("w", "x", "y0")}
         for name, enc in (("q5k", nq.Q5_K), ("iq4xs", nq.IQ4_XS)):
-            extras[f"{name}_gate_gemv"] = {k: v for k, v in bench_gemv(torch, nq, backend, stream, enc, 17408, 5120,
-                                                                       args.steps, args.warmup).items()
-                                           if k not in ("w", "x", "y0")}
-        if not only or "prefill" in only:
-            extras["prefill_q6k_down_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q6_K, 5120, 17408, 4096)
-            extras["prefill_q4k_gate_m512"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120, 512)
+            extras[f"{name}_gate_gemv"] = public(bench_gemv(torch, nq, backend, stream, enc, 17408, 5120, fixed, 50, 2))
+        if want("prefill"):
             extras["prefill_q5k_gate_m4096"] = bench_gemm(torch, nq, backend, stream, nq.Q5_K, 17408, 5120, 4096)
             extras["prefill_iq4xs_gate_m4096"] = bench_gemm(torch, nq, backend, stream, nq.IQ4_XS, 17408, 5120, 4096)
-            for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
-                extras[f"verify_m8_q4k_gate_{kname}"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 17408, 5120,
-                                                                   8, reps=200, warmup=20, kernel=kid)
-            extras["verify_m8_q4k_down_tile"] = bench_gemm(torch, nq, backend, stream, nq.Q4_K, 5120, 17408, 8,
-                                                           reps=200, warmup=20)
             extras["verify_m8_q5k_gate_tile"] = bench_gemm(torch, nq, backend, stream, nq.Q5_K, 17408, 5120, 8,
-                                                           reps=200, warmup=20)
+                                                           reps=200, warmup=20, x_seed=4)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(g["w"], x_host, rows, columns, args.cpu_seconds)
+        cpu = cpu_baseline(g["w"], g["x"].cpu().numpy(), rows, columns, args.cpu_seconds)
         cpu.pop("y")
     kernel_s = g["us_per_launch"] / 1e6
+    value = g["weight_gbs"]
     result = {
         "metric": "Q4_K GEMV GB/s (% of HBM peak) @5120x17408 M=1; prefill GEMM TFLOPS @M=4096",
-        "value": round(g["wall_weight_gbs"], 2),
+        "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": g["launches"],
-        "warmup": args.warmup,
-        "ms_per_step": round(g["wall_s"] * 1e3 / g["launches"], 6),
+        "warmup": g["warmup_launches"],
+        "ms_per_step": round(g["event_ms"] / g["launches"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k x f32 -> f32 (fp32 accumulate)",
-        "data": "synthetic: W ~ N(0,0.02) seed 2 quantized to Q4_K by libnuq, x ~ N(0,1) seed 1",
+        "dtype": GEMV_DTYPE,
+        "data": f"synthetic: W ~ N(0,0.02) seed {seed} quantized to Q4_K by libnuq, x ~ N(0,1) seed 1",
         "config": {"workload": "configs[1]: Q4_K batch-1 GEMV gate/up 5120->17408 (N=17408, K=5120), "
-                               f"{g['copies']} rotating weight copies",
-                   "weight_bytes": g["weight_bytes"], "hbm_peak_frac": round(g["wall_weight_gbs"] / HBM_PEAK_GBS, 4),
-                   "parity_normwise": normwise},
+                               f"{g['copies']} rotating weight copies; value = weight bytes x steps / "
+                               "event-timed region (one graph replay of exactly `steps` launches)",
+                   "weight_bytes": g["weight_bytes"], "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
+                   "wall_weight_gbs": round(g["wall_weight_gbs"], 2), "parity": gcheck},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("gemv_q4k_17408x5120_traffic"), "kernel": "gemv_dma_kernel<12, 4, 2>",
+                     "traffic": measured_traffic(TRAFFIC_PROFILE),
+                     "traffic_source": f"profiles/{TRAFFIC_PROFILE}.md (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, "
+                                       "copy-kernel calibrated; a profiled run, not this one)",
+                     "kernel": GEMV_KERNEL,
                      "us_per_launch": round(g["us_per_launch"], 3), "algo_bytes_per_launch": g["algo_bytes"]},
         "cpu_baseline": cpu,
     }
@@ -396,7 +489,10 @@ def main():
                              "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
                                           "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                           "frac": round(prefill["frac_f16_peak"], 4)},
+                             "check": prefill.get("check"),
                              "library_f16_gemm_same_shape_tflops": round(prefill["library"]["tflops"], 2)}
+    if configs:
+        result["configs"] = configs
     if extras:
         result["extras"] = extras
     backend.close()

@@ -85,8 +85,21 @@ typedef struct nuq_segment {
 nuq_context *nuq_create(int device, char *err, size_t cap);
 /* Replaces the backend's deinit. */
 void nuq_destroy(nuq_context *ctx);
-/* Work is enqueued on `stream` (a hipStream_t; NULL = the null stream). */
+/* Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ * When the stream changes, the new stream first waits for the work already
+ * enqueued on the old one (the context's workspace is shared by its calls),
+ * unless either stream is capturing a graph. */
 int nuq_set_stream(nuq_context *ctx, void *stream);
+/* The context's device workspace (verify K-range partials, prefill split
+ * partials, the SiLU pair's second GEMV) is allocated on the first call that
+ * wants it and grown as needed; nuq_create allocates none. A call that would
+ * grow it while its stream captures a graph takes its no-workspace route
+ * instead (same products). Callers that capture graphs may reserve it
+ * beforehand. No counterpart in the reference (Metal buffers are created per
+ * use, backends/metal/root.zig:62-86). */
+int nuq_reserve_workspace(nuq_context *ctx, uint64_t bytes);
+/* Bytes of workspace the context currently holds. */
+uint64_t nuq_workspace_bytes(const nuq_context *ctx);
 /* Replaces nu_metal_commit's wait (bridge.m:279-310): blocks until all work
  * enqueued on the context's stream has completed; reports device errors. */
 int nuq_sync(nuq_context *ctx);

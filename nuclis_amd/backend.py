@@ -108,7 +108,7 @@ EXPORTS = [
     "nuq_create", "nuq_destroy", "nuq_set_stream", "nuq_sync", "nuq_last_error", "nuq_set_generic_only",
     "nuq_validate_row", "nuq_embed", "nuq_dequant_range", "nuq_matvec", "nuq_matvec_rows", "nuq_matmul",
     "nuq_matmul_kernel", "nuq_matvec_segments", "nuq_argmax", "nuq_quantize_rows", "nuq_dequant_rows", "nuq_gemv",
-    "nuq_gemm", "nuq_topk", "nuq_penalize",
+    "nuq_gemm", "nuq_topk", "nuq_penalize", "nuq_reserve_workspace", "nuq_workspace_bytes",
 ]
 
 
@@ -126,6 +126,9 @@ def lib() -> ctypes.CDLL:
         L.nuq_destroy.argtypes = [vp]
         L.nuq_destroy.restype = None
         L.nuq_set_stream.argtypes = [vp, vp]
+        L.nuq_reserve_workspace.argtypes = [vp, u64]
+        L.nuq_workspace_bytes.argtypes = [vp]
+        L.nuq_workspace_bytes.restype = u64
         L.nuq_sync.argtypes = [vp]
         L.nuq_last_error.argtypes = [vp]
         L.nuq_last_error.restype = ctypes.c_char_p
@@ -233,14 +236,24 @@ class Backend:
     # -- plumbing -----------------------------------------------------------
     def _call(self, fn, *args) -> None:
         stream = self._torch.cuda.current_stream(self.device).cuda_stream
-        lib().nuq_set_stream(self._h, stream)
-        code = fn(self._h, *args)
+        # a change of stream makes the new one wait for the old one's work
+        # (the context's workspace is shared by its calls)
+        code = lib().nuq_set_stream(self._h, stream)
+        if code == 0:
+            code = fn(self._h, *args)
         if code != 0:
             _raise(code, lib().nuq_last_error(self._h).decode())
 
     def sync(self) -> None:
         """nu_metal_commit's wait (bridge.m:279-310)."""
         self._call(lib().nuq_sync)
+
+    def reserve_workspace(self, nbytes: int) -> None:
+        """Allocates the device workspace up front (for graph capture)."""
+        self._call(lib().nuq_reserve_workspace, nbytes)
+
+    def workspace_bytes(self) -> int:
+        return int(lib().nuq_workspace_bytes(self._h))
 
     def set_generic_only(self, enabled: bool) -> None:
         """Backend.generic_only (backends/metal/root.zig:99-102)."""

@@ -35,8 +35,12 @@ struct nuq_context {
     bool generic_only = false;
     std::string last_error;
     uint32_t *argmax_buf = nullptr;  // device: {index, nonfinite flag}
-    nuq::SplitScratch split{nullptr, 0};  // prefill K-split workspace
-    uint64_t *topk_keys = nullptr;        // partial top-k keys between passes
+    // F32 workspace of the verify K ranges, the prefill split partials and
+    // the SiLU pair's second GEMV: allocated on the first call that wants it
+    // and grown in whole 256 x 256 tiles (ensure_workspace)
+    nuq::SplitScratch split{nullptr, 0};
+    uint64_t *topk_keys = nullptr;  // partial top-k keys between passes
+    hipEvent_t handoff = nullptr;   // orders work across a stream change
 };
 
 namespace {
@@ -57,6 +61,34 @@ int fail(nuq_context *ctx, int code, const char *fmt, ...) {
 int hip_check(nuq_context *ctx, hipError_t e, const char *what) {
     if (e == hipSuccess) return NUQ_OK;
     return fail(ctx, NUQ_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Grows the context workspace to at least `floats` F32 values (whole 256 x
+// 256 tiles). Returns false, leaving it as it was, when the allocation fails
+// or the context's stream is capturing a graph (an allocation cannot be
+// captured): the caller's route then takes its no-workspace form, which
+// computes the same products. Growing waits for the device, since work in
+// flight may still use the old buffer.
+bool ensure_workspace(nuq_context *ctx, uint64_t floats) {
+    constexpr uint64_t TILE = 256 * 256;
+    if (floats == 0) return true;
+    const uint64_t tiles = (floats + TILE - 1) / TILE;
+    if (tiles <= ctx->split.tiles) return true;
+    if (tiles > 0xffffffffull) return false;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return false;
+    float *p = nullptr;
+    if (hipMalloc((void **)&p, tiles * TILE * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (ctx->split.work) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->split.work);
+    }
+    ctx->split.work = p;
+    ctx->split.tiles = (uint32_t)tiles;
+    return true;
 }
 
 int validate_row(uint32_t encoding, uint64_t byte_count, uint64_t element_count) {
@@ -191,6 +223,8 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
                                           (uint32_t)m->rows, (uint32_t)m->columns, x, f16, in_stride, out,
                                           out_stride, tokens),
                          "multi-token gemv launch");
+    (void)ensure_workspace(ctx, nuq::tile_workspace_floats(m->encoding, (uint32_t)m->rows, (uint32_t)m->columns,
+                                                           tokens, in_stride));
     return hip_check(ctx,
                      nuq::launch_tile(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
                                       (uint32_t)m->columns, x, f16, in_stride, out, out_stride, tokens, ctx->split),
@@ -234,14 +268,6 @@ nuq_context *nuq_create(int device, char *err, size_t cap) {
         delete ctx;
         return nullptr;
     }
-    // Four partial 256x256 F32 tiles per CU: 256 MiB on 256 CUs.
-    const uint32_t tiles = nuq::split_scratch_tiles();
-    if (hipMalloc((void **)&ctx->split.work, (size_t)tiles * 256 * 256 * sizeof(float)) != hipSuccess) {
-        report("hipMalloc of the prefill workspace failed");
-        nuq_destroy(ctx);
-        return nullptr;
-    }
-    ctx->split.tiles = tiles;
     if (hipMalloc((void **)&ctx->topk_keys, nuq::topk_scratch_keys() * sizeof(uint64_t)) != hipSuccess) {
         report("hipMalloc of the top-k scratch failed");
         nuq_destroy(ctx);
@@ -256,13 +282,45 @@ void nuq_destroy(nuq_context *ctx) {
     if (ctx->argmax_buf) (void)hipFree(ctx->argmax_buf);
     if (ctx->split.work) (void)hipFree(ctx->split.work);
     if (ctx->topk_keys) (void)hipFree(ctx->topk_keys);
+    if (ctx->handoff) (void)hipEventDestroy(ctx->handoff);
     delete ctx;
 }
 
 int nuq_set_stream(nuq_context *ctx, void *stream) {
     if (!ctx) return NUQ_INVALID_ARGUMENT;
-    ctx->stream = (hipStream_t)stream;
+    hipStream_t next = (hipStream_t)stream;
+    if (next != ctx->stream) {
+        // The context's workspace is shared by its calls: work on the new
+        // stream waits for what was enqueued on the old one. Skipped when
+        // either stream is capturing a graph (a capture cannot wait on work
+        // outside it); the caller orders captured work itself.
+        hipStreamCaptureStatus a = hipStreamCaptureStatusNone, b = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &a) == hipSuccess && hipStreamIsCapturing(next, &b) == hipSuccess &&
+            a == hipStreamCaptureStatusNone && b == hipStreamCaptureStatusNone) {
+            if (!ctx->handoff) {
+                int e = hip_check(ctx, hipEventCreateWithFlags(&ctx->handoff, hipEventDisableTiming), "event");
+                if (e) return e;
+            }
+            int e = hip_check(ctx, hipEventRecord(ctx->handoff, ctx->stream), "stream handoff record");
+            if (!e) e = hip_check(ctx, hipStreamWaitEvent(next, ctx->handoff, 0), "stream handoff wait");
+            if (e) return e;
+        }
+        ctx->stream = next;
+    }
     return NUQ_OK;
+}
+
+int nuq_reserve_workspace(nuq_context *ctx, uint64_t bytes) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    (void)hipSetDevice(ctx->device);
+    if (!ensure_workspace(ctx, (bytes + sizeof(float) - 1) / sizeof(float)))
+        return fail(ctx, NUQ_DEVICE_ERROR, "workspace of %llu bytes could not be allocated (or the stream is capturing)",
+                    (unsigned long long)bytes);
+    return NUQ_OK;
+}
+
+uint64_t nuq_workspace_bytes(const nuq_context *ctx) {
+    return ctx ? (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float) : 0;
 }
 
 int nuq_sync(nuq_context *ctx) {
@@ -443,6 +501,7 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
     // epilogue than as one merged row-per-wave pass.
     const bool pair_split = mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only &&
                             segments[0].matrix.rows >= PAIR_SPLIT_ROWS &&
+                            ensure_workspace(ctx, segments[0].matrix.rows) &&
                             segments[0].matrix.rows * sizeof(float) <=
                                 (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float);
     // Segments of one encoding and row stride (q/k/v, gate/up) run as one

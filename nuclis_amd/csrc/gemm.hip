@@ -780,6 +780,35 @@ static uint32_t compute_units() {
     return cached;
 }
 
+// The prefill's K-split plan (see launch_prefill): `full` whole tiles, then
+// `tail` tiles split `splits` ways, needing tail * splits partial tiles of
+// workspace; no split when the workspace holds fewer than that
+// (max_tiles = 0: none).
+static void prefill_split_plan(uint32_t tiles, uint32_t columns, uint32_t cus, uint64_t max_tiles, uint32_t *full,
+                               uint32_t *tail, uint32_t *splits) {
+    *full = tiles;
+    *tail = 0;
+    *splits = 1;
+    const uint32_t rem = tiles % cus;
+    if (rem == 0 || columns % 256 != 0 || max_tiles == 0) return;
+    const uint32_t nb = columns / 256;
+    const double whole = (double)nb + 1.0;
+    double best = 0.85 * whole;
+    for (uint32_t sp = 2; sp <= std::min(nb, 16u); ++sp) {
+        if ((uint64_t)rem * sp > max_tiles) break;
+        const double rounds = (double)((rem * sp + cus - 1) / cus);
+        const double cost = rounds * ((double)((nb + sp - 1) / sp) + 1.0) + (double)rem * sp / 100.0 + 0.3;
+        if (cost < best) {
+            best = cost;
+            *splits = sp;
+        }
+    }
+    if (*splits > 1) {
+        *full = tiles - rem;
+        *tail = rem;
+    }
+}
+
 template <uint32_t ENC>
 static hipError_t launch_prefill(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
                                  const void *x, uint32_t x_f16, uint64_t in_stride, float *y, uint64_t out_stride,
@@ -795,26 +824,8 @@ static hipError_t launch_prefill(hipStream_t s, const uint8_t *w, uint64_t strid
     // tiles of 256 KiB per split tile (about 1/100 of a unit each, plus a
     // launch). A split is taken only when it is predicted 15% faster (on
     // MI355X it does not pay for Q4_K 17408 x 5120 at 512 tokens).
-    uint32_t full = tiles, tail = 0, splits = 1;
-    const uint32_t rem = tiles % cus;
-    if (rem != 0 && columns % 256 == 0 && scratch.work != nullptr) {
-        const uint32_t nb = columns / 256;
-        const double whole = (double)nb + 1.0;
-        double best = 0.85 * whole;
-        for (uint32_t sp = 2; sp <= std::min(nb, 16u); ++sp) {
-            if ((uint64_t)rem * sp > scratch.tiles) break;
-            const double rounds = (double)((rem * sp + cus - 1) / cus);
-            const double cost = rounds * ((double)((nb + sp - 1) / sp) + 1.0) + (double)rem * sp / 100.0 + 0.3;
-            if (cost < best) {
-                best = cost;
-                splits = sp;
-            }
-        }
-        if (splits > 1) {
-            full = tiles - rem;
-            tail = rem;
-        }
-    }
+    uint32_t full, tail, splits;
+    prefill_split_plan(tiles, columns, cus, scratch.work != nullptr ? scratch.tiles : 0, &full, &tail, &splits);
     const uint32_t grid = full + tail * splits;
     const size_t lds = (size_t)2 * (PF_BM + PF_BN) * LDS_PITCH * sizeof(_Float16);
 #define NUQ_PF_LAUNCH(NW_)                                                                                       \
@@ -1897,6 +1908,26 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 
 
 uint32_t split_scratch_tiles() { return 4 * compute_units(); }
+
+uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t columns, uint32_t tokens,
+                               uint64_t in_stride) {
+    if (tokens <= 16 && columns % 256 == 0) {
+        // the streamed verify tile's K ranges (Q4_K / Q5_K rows longer than
+        // 2 * MAXW blocks), one F32 partial per range, token and row
+        constexpr uint32_t MAXW = vd_max_waves<2>();
+        const uint32_t nblocks = columns / 256;
+        if ((encoding != 12 && encoding != 13) || nblocks <= 2 * MAXW || rows < 16) return 0;
+        return (uint64_t)((nblocks + 2 * MAXW - 1) / (2 * MAXW)) * tokens * rows;
+    }
+    if (tokens > 128 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {  // as launch_tile routes
+        const uint32_t cus = compute_units();
+        const uint32_t tiles = ((tokens + PF_BM - 1) / PF_BM) * ((rows + PF_BN - 1) / PF_BN);
+        uint32_t full, tail, splits;
+        prefill_split_plan(tiles, columns, cus, split_scratch_tiles(), &full, &tail, &splits);
+        return (uint64_t)tail * splits * PF_BM * PF_BN;
+    }
+    return 0;
+}
 
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,

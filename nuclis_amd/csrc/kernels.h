@@ -77,5 +77,10 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);
 uint32_t split_scratch_tiles();
+// F32 workspace the tile route of this call would use (verify K ranges or
+// prefill split partials); 0 when it needs none. A smaller workspace makes
+// the route fall back (fewer splits, or the register verify tile).
+uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t columns, uint32_t tokens,
+                               uint64_t in_stride);
 
 }  // namespace nuq

@@ -45,3 +45,18 @@ def write_gguf(path, tensors, metadata=None, alignment=32) -> None:
     with open(path, "wb") as f:
         f.write(out)
         f.write(data)
+
+
+# Seeds of the benchmark configurations (BASELINE.json `configs`), shared by
+# the config tests and bench.py: name -> (encoding, rows N, columns K, weight
+# seed). Activations: x seed 1 for the GEMVs, seed 4 for the M=8 verify
+# activations, seed 5 for the prefill activations (N(0,1), f16 for the
+# tiles).
+CONFIGS = {
+    "c1_q8_0": (8, 4096, 4096, 0),       # configs[0]: W from seed 0
+    "c2_gate": (12, 17408, 5120, 2),     # configs[1] gate/up 5120 -> 17408
+    "c2_down": (12, 5120, 17408, 3),     # configs[1] down 17408 -> 5120
+    "c5_gate": (12, 17408, 5120, 2),     # configs[4] Q4_K gate
+    "c5_down": (14, 5120, 17408, 3),     # configs[4] Q6_K down
+}
+X_SEED_GEMV, X_SEED_VERIFY, X_SEED_PREFILL = 1, 4, 5

@@ -8,3 +8,15 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libnuq.so on cuda:0)")
+
+
+def pytest_terminal_summary(terminalreporter):
+    try:
+        from tests.gpu_util import WORST
+    except Exception:
+        return
+    if not WORST:
+        return
+    terminalreporter.write_line("worst observed |gpu - oracle| / sum|w*x| per check (bound factor k):")
+    for label, (ratio, k) in sorted(WORST.items()):
+        terminalreporter.write_line(f"  {label:24s} {ratio:.3e}  (k = {k:.0e})")

@@ -9,10 +9,15 @@ Tolerances (stated where they are used):
   * integer-dot GEMV (activations rounded to 16 bits of their 32-value
     slice maximum before the exact integer dot): the F32 bound plus the
     rigorous rounding term sum_c |w[r,c]| * max|x slice(c)| / 65278;
-  * f16 MFMA tile: weights (and F32 activations) are rounded to f16, each
-    term then carries at most 2^-11 relative error per rounded operand, so
-    |gpu - ref| <= 2e-3 * sum|w*x| + 1e-6 per output, plus the same 2e-3
-    normwise bound.
+  * f16 MFMA tiles (verify, 128x128 and prefill): weights (and F32
+    activations) are rounded to f16, so each term carries at most 2^-11
+    relative error per rounded operand; the bound is the reference's own for
+    its half tiles, |gpu - ref| <= 2e-4 * sum|w*x| + 1e-6 per output
+    (metal-check.zig:3779, 3826, 4424), plus the same 2e-3 normwise bound.
+
+check_close records the worst observed |gpu - ref| / sum|w*x| per label;
+conftest prints the table at the end of the session, so the margin under
+each bound is visible in the test log.
 """
 import numpy as np
 
@@ -41,6 +46,12 @@ def xq_mass(encoding, w_bytes, rows, columns, x):
     return (amax / 65278.0) @ np.abs(dec).T
 
 
+F32_K = 4e-6   # F32 arithmetic (metal-check.zig:3976)
+F16_K = 2e-4   # half tiles (metal-check.zig:4424)
+
+WORST = {}   # label -> (worst |d| / mass, bound factor k)
+
+
 def check_close(got, want, mass_, k, label="", extra=0.0):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
@@ -51,6 +62,11 @@ def check_close(got, want, mass_, k, label="", extra=0.0):
     worst = np.unravel_index(np.argmax(err - bound), err.shape)
     assert np.all(err <= bound), (f"{label}: |d|={err[worst]:.3e} > bound {bound[worst]:.3e} at {worst} "
                                   f"(got {got[worst]}, want {want[worst]})")
+    m = np.asarray(mass_, np.float64)
+    ratio = float(np.max(np.where(m > 0, err / np.where(m > 0, m, 1.0), 0.0))) if err.size else 0.0
+    key = label.split(" ")[0] if label else "unlabelled"
+    if ratio >= WORST.get(key, (-1.0, k))[0]:
+        WORST[key] = (ratio, k)
     normwise = err.max() / max(np.abs(want).max(), 1e-30)
     assert normwise <= 2e-3, f"{label}: normwise {normwise:.3e}"
     return normwise

@@ -1,34 +1,23 @@
 """Configuration 3: one 27B-shaped decode layer + Q6_K lm_head through the
 HIP path, against the CPU oracle's composition of the same step. The greedy
 token must be identical (sampling/root.zig:226-239); logits are also checked
-normwise (2e-3). The CPU side follows the reference's operations: matvecs
-with F64 accumulation (cpu/root.zig:112-165) and silu(x) = f32(x * logistic(x))
-in F64 (cpu/vector.zig:178-181)."""
+normwise (2e-3). The CPU side (oracle/layer_oracle.py) follows the reference's
+operations: matvecs with F64 accumulation (cpu/root.zig:112-165) and
+silu(x) = f32(x * logistic(x)) in F64 (cpu/vector.zig:178-181)."""
 import numpy as np
 import pytest
 
 import nuclis_amd as nq
 from nuclis_amd import layer as L
 from nuclis_amd.synth import gaussian
+from oracle import layer_oracle
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
 
 def cpu_step(weights, x):
-    def mv(name, v):
-        enc, _, cols, _ = L.SHAPES[name]
-        w = weights[name]
-        return orc.matvec(enc, w.shape[0], cols, w, v)
-    v = mv("v", x)
-    idx = (np.arange(L.Q_ROWS) // (L.HEAD_DIM * L.GQA)) * L.HEAD_DIM + np.arange(L.Q_ROWS) % L.HEAD_DIM
-    h1 = (x + mv("o", v[idx])).astype(np.float32)
-    g = mv("gate", h1).astype(np.float64)
-    u = mv("up", h1)
-    silu = (g / (1.0 + np.exp(-g))).astype(np.float32)
-    act = (silu * u).astype(np.float32)
-    h2 = (h1 + mv("down", act)).astype(np.float32)
-    return mv("lm_head", h2)
+    return layer_oracle.cpu_step(L.SHAPES, weights, x)
 
 
 @pytest.mark.parametrize("vocab_fraction", [1.0])
