@@ -42,8 +42,8 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
 MALL_BYTES = 256 << 20
 GEMV_KERNEL = "gemv_dma_kernel<12, 4, 2>"
-GEMV_DTYPE = ("q4_k codes x f32 activations rounded to 16-bit fixed point per 32-value slice "
-              "(int8 byte planes, exact int32 dot) -> f32 scale/accumulate")
+GEMV_DTYPE = ("q4_k codes x f32 activations carried as 24-bit fixed point per 32-value slice "
+              "(three int8 byte planes, exact int32 dot; F32-mantissa precision) -> f32 scale/accumulate")
 
 
 def parse():
@@ -217,8 +217,7 @@ def public(d):
 
 def check_gemv(orc, g, encoding, rows, columns, stride_rows=97):
     """The timed GEMV's output against the oracle on every stride_rows-th row:
-    the F32 bound |d| <= 4e-6 * sum|w*x| + 1e-6 plus the activation rounding
-    term of the integer-dot kernel, and the normwise 2e-3."""
+    the F32 bound |d| <= 4e-6 * sum|w*x| + 1e-6 (metal-check.zig:3976)."""
     x_host = g["x"].cpu().numpy()
     sample = np.arange(0, rows, stride_rows)
     w = np.ascontiguousarray(g["w"][sample])
@@ -226,8 +225,7 @@ def check_gemv(orc, g, encoding, rows, columns, stride_rows=97):
     got = g["y0"].cpu().numpy()[sample].astype(np.float64)
     dec = np.abs(orc.decode_matrix(encoding, w, sample.size, columns).astype(np.float64))
     m = dec @ np.abs(x_host.astype(np.float64))
-    amax = np.repeat(np.abs(x_host.astype(np.float64)).reshape(-1, 32).max(-1), 32)
-    bound = 4e-6 * m + dec @ (amax / 65278.0) + 1e-6
+    bound = 4e-6 * m + 1e-6
     err = np.abs(got - ref)
     assert np.all(err <= bound), f"GEMV enc {encoding} {rows}x{columns} outside the bound"
     return {"rows_checked": int(sample.size), "normwise": float(err.max() / np.abs(ref).max()),

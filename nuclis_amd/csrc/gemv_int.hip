@@ -7,15 +7,17 @@
 // int32 accumulation.
 //
 // Activations: every lane keeps a fixed slice of x for the whole kernel
-// (the K-split below), so it quantises that slice once: per 32-value slice,
-// scale s = max|x| / 32639 and x16 = rint(x / s), split exactly into two
-// signed bytes x16 = 256*xh + xl (xl in [-128, 127], xh in [-128, 127]).
-// A code q then contributes q * x16 = 256 * (q * xh) + q * xl, i.e. two
-// dot4 accumulations. The only approximation against the F32 reference is
-// x's rounding to 16 bits relative to its slice maximum (|error| <=
-// max|x| / 65278 per element); sums of codes are exact and the per-group
-// affine terms (scale, minimum) are applied in F32. Non-finite activations
-// make the affected outputs NaN.
+// (the K-split below), so it converts that slice once to 24-bit fixed point,
+// as many significant bits as an F32 mantissa: per 32-value slice, scale
+// s = max|x| / 8355711 and x24 = rint(x / s), split exactly into three
+// signed bytes x24 = 65536*xh + 256*xm + xl (each in [-128, 127]). A code q
+// then contributes q*x24 = 65536*(q*xh) + 256*(q*xm) + q*xl: three dot4
+// accumulations, each exact in int32. The only approximation before the
+// F32 scale and accumulate is x's rounding to 24 bits of its slice maximum
+// (|error| <= max|x| / 16711422 + a rounding of the F32 product, about
+// 1.2e-7 * max|x| per element); the per-group affine terms (scale,
+// minimum) are applied in F32. Non-finite activations make the affected
+// outputs NaN.
 //
 // Layout (K-split, persistent rows): a workgroup of W waves owns a range of
 // rows; wave w owns the block range [4P*w, 4P*w + 4P) of every row, so its
@@ -39,19 +41,24 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// 32 consecutive activations as two byte planes (8 dwords each), with the
+// 32 consecutive activations as three byte planes (8 dwords each), with the
 // slice scale and the F32 sum of the original values.
 struct XSlice {
-    uint32_t hi[8], lo[8];
+    uint32_t hi[8], mid[8], lo[8];
     float scale;
     float sum;
-    int isum;      // sum of x16 (used by biased codes)
     float poison;  // NaN when the slice holds a non-finite value, else 0
-    int hsum;      // sum of x16 over values 0-15 (Q6_K's 16-value scales; registers only)
+    // Q6_K only (registers): 32 * sum(x24) over values 0-15 and 16-31
+    float bias[2];
 };
 
-// LDS image of one quantised slice: 16 plane dwords + scale, sum, isum, poison.
-constexpr int SLICE_WORDS = 20;
+// LDS image of one quantised slice: 24 plane dwords + scale, sum, poison, pad.
+constexpr int SLICE_WORDS = 28;
+constexpr float X24_MAX = 8355711.f;  // 127 * (65536 + 256 + 1): every byte of the split in [-128, 127]
+
+// q*x24 from the three plane sums: 65536*h + (256*m + l); the parenthesis
+// is an exact int32 for every encoding's codes, then one F32 rounding.
+__device__ __forceinline__ float combine3(int h, int m, int l) { return fmaf((float)h, 65536.f, (float)(m * 256 + l)); }
 
 // Cooperative quantisation: lane pair (2s, 2s+1) quantises slice s (32
 // values at xs[s]) of the wave's slice list, 16 values per lane; the two
@@ -119,83 +126,110 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
     // the pair's halves: lane ^ 1
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
     const float other_sum = __shfl_xor(sum, 1, 64);
-    finite = finite && (__shfl_xor((int)finite, 1, 64) != 0);
-    const float scale = amax / 32639.f;
-    const float inv = amax > 0.f ? 32639.f / amax : 0.f;
-    int isum = 0;
-    uint32_t hw[4], lw[4];
+    // every lane must take part in the exchange: written as `finite && shfl`,
+    // the exchange would run only in finite lanes and read a stale value
+    // from a non-finite partner
+    const int partner_finite = __shfl_xor((int)finite, 1, 64);
+    finite = finite && partner_finite != 0;
+    const float scale = amax / X24_MAX;
+    const float inv = amax > 0.f ? X24_MAX / amax : 0.f;
+    uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        uint32_t h = 0, l = 0;
+        uint32_t h = 0, m = 0, l = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            int q = finite ? (int)rintf(v[4 * k + e] * inv) : 0;
-            isum += q;
+            // |q| <= 8355711: q = 65536*hi + 256*mi + lo with every part in [-128, 127]
+            const int q = finite ? min(max((int)rintf(v[4 * k + e] * inv), -8355711), 8355711) : 0;
             const int lo = ((q + 128) & 255) - 128;
-            const int hi = (q - lo) >> 8;
+            const int q1 = (q - lo) >> 8;
+            const int mi = ((q1 + 128) & 255) - 128;
+            const int hi = (q1 - mi) >> 8;
             h |= (uint32_t)(hi & 255) << (8 * e);
+            m |= (uint32_t)(mi & 255) << (8 * e);
             l |= (uint32_t)(lo & 255) << (8 * e);
         }
         hw[k] = h;
+        mw[k] = m;
         lw[k] = l;
     }
-    isum += __shfl_xor(isum, 1, 64);
-    // words: hi plane 0..7, lo plane 8..15, then scale, sum (lower half first, as
-    // the summation order), isum, poison
-    const uint32_t t0 = __float_as_uint(scale), t1 = __float_as_uint(sum + other_sum), t2 = (uint32_t)isum,
-                   t3 = finite ? 0u : 0x7fc00000u;
+    // words: hi plane 0..7, mid plane 8..15, lo plane 16..23, then scale, sum
+    // (lower half first, as the summation order), poison
+    const uint32_t t0 = __float_as_uint(scale), t1 = __float_as_uint(sum + other_sum),
+                   t2 = finite ? 0u : 0x7fc00000u;
     if constexpr (ASM_LDS) {
         lds_store4(lds + 4 * half, hw[0], hw[1], hw[2], hw[3]);
-        lds_store4(lds + 8 + 4 * half, lw[0], lw[1], lw[2], lw[3]);
-        if (half == 0) lds_store4(lds + 16, t0, t1, t2, t3);
+        lds_store4(lds + 8 + 4 * half, mw[0], mw[1], mw[2], mw[3]);
+        lds_store4(lds + 16 + 4 * half, lw[0], lw[1], lw[2], lw[3]);
+        if (half == 0) lds_store4(lds + 24, t0, t1, t2, 0u);
     } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             lds[4 * half + k] = hw[k];
-            lds[8 + 4 * half + k] = lw[k];
+            lds[8 + 4 * half + k] = mw[k];
+            lds[16 + 4 * half + k] = lw[k];
         }
         if (half == 0) {
-            lds[16] = t0;
-            lds[17] = t1;
-            lds[18] = t2;
-            lds[19] = t3;
+            lds[24] = t0;
+            lds[25] = t1;
+            lds[26] = t2;
+            lds[27] = 0u;
         }
     }
 }
 
 // read_slice through asm (see lds_store4); waits for its own reads.
 __device__ __forceinline__ void read_slice_asm(const uint32_t *lds, XSlice &s) {
-    u32x4_t a, b, c, d, e;
+    u32x4_t p[7];
     asm volatile(
-        "ds_read_b128 %0, %5\n\t"
-        "ds_read_b128 %1, %5 offset:16\n\t"
-        "ds_read_b128 %2, %5 offset:32\n\t"
-        "ds_read_b128 %3, %5 offset:48\n\t"
-        "ds_read_b128 %4, %5 offset:64\n\t"
+        "ds_read_b128 %0, %7\n\t"
+        "ds_read_b128 %1, %7 offset:16\n\t"
+        "ds_read_b128 %2, %7 offset:32\n\t"
+        "ds_read_b128 %3, %7 offset:48\n\t"
+        "ds_read_b128 %4, %7 offset:64\n\t"
+        "ds_read_b128 %5, %7 offset:80\n\t"
+        "ds_read_b128 %6, %7 offset:96\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d), "=&v"(e)
+        : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(p[4]), "=&v"(p[5]), "=&v"(p[6])
         : "v"(lds_addr(lds))
         : "memory");
-    s.hi[0] = a.x; s.hi[1] = a.y; s.hi[2] = a.z; s.hi[3] = a.w;
-    s.hi[4] = b.x; s.hi[5] = b.y; s.hi[6] = b.z; s.hi[7] = b.w;
-    s.lo[0] = c.x; s.lo[1] = c.y; s.lo[2] = c.z; s.lo[3] = c.w;
-    s.lo[4] = d.x; s.lo[5] = d.y; s.lo[6] = d.z; s.lo[7] = d.w;
-    s.scale = __uint_as_float(e.x);
-    s.sum = __uint_as_float(e.y);
-    s.isum = (int)e.z;
-    s.poison = __uint_as_float(e.w);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        s.hi[4 * k] = p[k].x; s.hi[4 * k + 1] = p[k].y; s.hi[4 * k + 2] = p[k].z; s.hi[4 * k + 3] = p[k].w;
+        s.mid[4 * k] = p[2 + k].x; s.mid[4 * k + 1] = p[2 + k].y; s.mid[4 * k + 2] = p[2 + k].z; s.mid[4 * k + 3] = p[2 + k].w;
+        s.lo[4 * k] = p[4 + k].x; s.lo[4 * k + 1] = p[4 + k].y; s.lo[4 * k + 2] = p[4 + k].z; s.lo[4 * k + 3] = p[4 + k].w;
+    }
+    s.scale = __uint_as_float(p[6].x);
+    s.sum = __uint_as_float(p[6].y);
+    s.poison = __uint_as_float(p[6].z);
 }
 
 __device__ __forceinline__ void read_slice(const uint32_t *lds, XSlice &s) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         s.hi[k] = lds[k];
-        s.lo[k] = lds[8 + k];
+        s.mid[k] = lds[8 + k];
+        s.lo[k] = lds[16 + k];
     }
-    s.scale = __uint_as_float(lds[16]);
-    s.sum = __uint_as_float(lds[17]);
-    s.isum = (int)lds[18];
-    s.poison = __uint_as_float(lds[19]);
+    s.scale = __uint_as_float(lds[24]);
+    s.sum = __uint_as_float(lds[25]);
+    s.poison = __uint_as_float(lds[26]);
+}
+
+// Q6_K's -32 bias per 16-value half of a slice: 32 * sum(x24), from the
+// planes' exact integer sums, rounded once to F32.
+__device__ __forceinline__ void plane_sums(XSlice &s) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        int h = 0, m = 0, l = 0;
+#pragma unroll
+        for (int k = 4 * half; k < 4 * half + 4; ++k) {
+            h = dot4(s.hi[k], 0x01010101u, h);
+            m = dot4(s.mid[k], 0x01010101u, m);
+            l = dot4(s.lo[k], 0x01010101u, l);
+        }
+        s.bias[half] = 32.f * combine3(h, m, l);
+    }
 }
 
 // Q4_K scales/minima of the pair (2j, 2j+1) as floats (quant/decode.zig:155-158),
@@ -221,18 +255,20 @@ __device__ __forceinline__ void q4k_pair_f(uint32_t s0, uint32_t s1, uint32_t s2
 __device__ __forceinline__ float q4k_lane(const uint4 hdr, const uint4 q0, const uint4 q1, const XSlice &A,
                                           const XSlice &B, uint32_t shift, bool direct) {
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int ah = 0, al = 0, bh = 0, bl = 0;
+    int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t lo = w[k] & 0x0f0f0f0fu;
         const uint32_t hi = (w[k] >> 4) & 0x0f0f0f0fu;
         ah = dot4(lo, A.hi[k], ah);
+        am = dot4(lo, A.mid[k], am);
         al = dot4(lo, A.lo[k], al);
         bh = dot4(hi, B.hi[k], bh);
+        bm = dot4(hi, B.mid[k], bm);
         bl = dot4(hi, B.lo[k], bl);
     }
-    const float ia = (float)(ah * 256 + al);
-    const float ib = (float)(bh * 256 + bl);
+    const float ia = combine3(ah, am, al);
+    const float ib = combine3(bh, bm, bl);
     const float d = half_bits(hdr.x & 0xffffu), dmin = half_bits(hdr.x >> 16);
     float sa, ma, sb, mb;
     q4k_pair_f(hdr.y, hdr.z, hdr.w, shift, direct, sa, ma, sb, mb);
@@ -446,17 +482,19 @@ struct GdEnc<13> {  // Q5_K: header, the 32 high-plane bytes, the pair's 32 code
                                          bool direct) const {
         const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const uint32_t hb[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
-        int ah = 0, al = 0, bh = 0, bl = 0;
+        int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t lo = (w[k] & 0x0f0f0f0fu) | (((hb[k] >> (2 * j)) & 0x01010101u) << 4);
             const uint32_t hi = ((w[k] >> 4) & 0x0f0f0f0fu) | (((hb[k] >> (2 * j + 1)) & 0x01010101u) << 4);
             ah = dot4(lo, A.hi[k], ah);
+            am = dot4(lo, A.mid[k], am);
             al = dot4(lo, A.lo[k], al);
             bh = dot4(hi, B.hi[k], bh);
+            bm = dot4(hi, B.mid[k], bm);
             bl = dot4(hi, B.lo[k], bl);
         }
-        const float ia = (float)(ah * 256 + al), ib = (float)(bh * 256 + bl);
+        const float ia = combine3(ah, am, al), ib = combine3(bh, bm, bl);
         const float d = half_bits(h.x & 0xffffu), dmin = half_bits(h.x >> 16);
         float sa, ma, sb, mb;
         q4k_pair_f(h.y, h.z, h.w, shift, direct, sa, ma, sb, mb);
@@ -545,32 +583,29 @@ struct GdEnc<14> {  // Q6_K: the half's 64 code bytes, its 32 high-bit bytes, 4 
         const uint32_t lb[8] = {l2.x, l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w};
         const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         // Codes stay unsigned (0..63, also valid signed bytes); the -32 bias
-        // comes off each 16-value sum as 32 * sum(x16), so every integer
-        // below is the same as with the biased codes.
-        int a0h = 0, a0l = 0, a1h = 0, a1l = 0, b0h = 0, b0l = 0, b1h = 0, b1l = 0;
+        // comes off each 16-value sum in F32 as 32 * sum(x24) of those values.
+        int a0[3] = {0, 0, 0}, a1[3] = {0, 0, 0}, b0[3] = {0, 0, 0}, b1[3] = {0, 0, 0};
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t hq = hb[k];
             const uint32_t ua = (la[k] & 0x0f0f0f0fu) | ((hq << 4) & 0x30303030u);
             const uint32_t ub = (lb[k] & 0x0f0f0f0fu) | ((hq << 2) & 0x30303030u);
-            if (k < 4) {
-                a0h = dot4(ua, A.hi[k], a0h);
-                a0l = dot4(ua, A.lo[k], a0l);
-                b0h = dot4(ub, B.hi[k], b0h);
-                b0l = dot4(ub, B.lo[k], b0l);
-            } else {
-                a1h = dot4(ua, A.hi[k], a1h);
-                a1l = dot4(ua, A.lo[k], a1l);
-                b1h = dot4(ub, B.hi[k], b1h);
-                b1l = dot4(ub, B.lo[k], b1l);
-            }
+            int *ra = k < 4 ? a0 : a1, *rb = k < 4 ? b0 : b1;
+            ra[0] = dot4(ua, A.hi[k], ra[0]);
+            ra[1] = dot4(ua, A.mid[k], ra[1]);
+            ra[2] = dot4(ua, A.lo[k], ra[2]);
+            rb[0] = dot4(ub, B.hi[k], rb[0]);
+            rb[1] = dot4(ub, B.mid[k], rb[1]);
+            rb[2] = dot4(ub, B.lo[k], rb[2]);
         }
         const float s0 = (float)(int8_t)(sc & 0xffu), s1 = (float)(int8_t)((sc >> 8) & 0xffu);
         const float s2 = (float)(int8_t)((sc >> 16) & 0xffu), s3 = (float)(int8_t)(sc >> 24);
-        const int ia0 = a0h * 256 + a0l - 32 * A.hsum, ia1 = a1h * 256 + a1l - 32 * (A.isum - A.hsum);
-        const int ib0 = b0h * 256 + b0l - 32 * B.hsum, ib1 = b1h * 256 + b1l - 32 * (B.isum - B.hsum);
-        const float ta = fmaf(s0, (float)ia0, s1 * (float)ia1);
-        const float tb = fmaf(s2, (float)ib0, s3 * (float)ib1);
+        const float ia0 = combine3(a0[0], a0[1], a0[2]) - A.bias[0];
+        const float ia1 = combine3(a1[0], a1[1], a1[2]) - A.bias[1];
+        const float ib0 = combine3(b0[0], b0[1], b0[2]) - B.bias[0];
+        const float ib1 = combine3(b1[0], b1[1], b1[2]) - B.bias[1];
+        const float ta = fmaf(s0, ia0, s1 * ia1);
+        const float tb = fmaf(s2, ib0, s3 * ib1);
         return half_bits(d16) * fmaf(A.scale, ta, B.scale * tb);
     }
 };
@@ -621,16 +656,18 @@ struct GdEnc<8> {  // Q8_0: eight 34-byte blocks (256 values) as one unit; lane 
     // w = d * q per 32-value block (quant/decode.zig:57-63): the exact
     // integer sums of q * x16 scaled by d and the slice scale in F32
     __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t, uint32_t, bool) const {
-        int ah = 0, al = 0, bh = 0, bl = 0;
+        int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             ah = dot4(qa[k], A.hi[k], ah);
+            am = dot4(qa[k], A.mid[k], am);
             al = dot4(qa[k], A.lo[k], al);
             bh = dot4(qb[k], B.hi[k], bh);
+            bm = dot4(qb[k], B.mid[k], bm);
             bl = dot4(qb[k], B.lo[k], bl);
         }
         const float ta = half_bits(da) * A.scale, tb = half_bits(db) * B.scale;
-        return fmaf(ta, (float)(ah * 256 + al), tb * (float)(bh * 256 + bl));
+        return fmaf(ta, combine3(ah, am, al), tb * combine3(bh, bm, bl));
     }
 };
 
@@ -660,21 +697,25 @@ struct GdEnc<23> {  // IQ4_XS: 8-byte header + the pair's 32 code bytes (8-byte 
     // (quant/decode.zig:213-228); codes map to signed bytes by iq4_lookup.
     __device__ __forceinline__ float dot(const XSlice &A, const XSlice &B, uint32_t j, uint32_t, bool) const {
         const uint32_t wa[4] = {qa.x, qa.y, qa.z, qa.w}, wb[4] = {qb.x, qb.y, qb.z, qb.w};
-        int ah = 0, al = 0, bh = 0, bl = 0;
+        int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t la = iq4_lookup(wa[m] & 0x0f0f0f0fu), ua = iq4_lookup((wa[m] >> 4) & 0x0f0f0f0fu);
             const uint32_t lb = iq4_lookup(wb[m] & 0x0f0f0f0fu), ub = iq4_lookup((wb[m] >> 4) & 0x0f0f0f0fu);
             ah = dot4(la, A.hi[m], ah);
+            am = dot4(la, A.mid[m], am);
             al = dot4(la, A.lo[m], al);
             ah = dot4(ua, A.hi[4 + m], ah);
+            am = dot4(ua, A.mid[4 + m], am);
             al = dot4(ua, A.lo[4 + m], al);
             bh = dot4(lb, B.hi[m], bh);
+            bm = dot4(lb, B.mid[m], bm);
             bl = dot4(lb, B.lo[m], bl);
             bh = dot4(ub, B.hi[4 + m], bh);
+            bm = dot4(ub, B.mid[4 + m], bm);
             bl = dot4(ub, B.lo[4 + m], bl);
         }
-        const float ia = (float)(ah * 256 + al), ib = (float)(bh * 256 + bl);
+        const float ia = combine3(ah, am, al), ib = combine3(bh, bm, bl);
         const uint32_t sl = (h1 >> (8 * j)) & 0xffu, sh = h0 >> 16;
         const int sa = (int)((sl & 15u) | (((sh >> (4 * j)) & 3u) << 4)) - 32;
         const int sb = (int)((sl >> 4) | (((sh >> (4 * j + 2)) & 3u) << 4)) - 32;
@@ -702,8 +743,14 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Workgroup size cap of the DMA kernel: 16 waves, except Q6_K, whose lanes
+// hold more bytes per block (the alignment shifts) and so take 12 waves,
+// keeping its registers (up to 170) clear of spills.
+template <uint32_t ENC>
+constexpr int gd_threads() { return ENC == 14 ? 768 : GI_WG_THREADS; }
+
 template <uint32_t ENC, int SLOTS, int D>
-__global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+__global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
                                                                       const float *__restrict__ x,
@@ -824,17 +871,8 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_dma_kernel(const uint8_t *
     read_slice_asm(slices + (bb * 8 + 2 * j) * SLICE_WORDS, xa);
     read_slice_asm(slices + (bb * 8 + 2 * j + 1) * SLICE_WORDS, xb);
     if constexpr (ENC == 14) {
-        // sum of x16 = 256 xh + xl over values 0-15 (the first 4 plane dwords)
-        int ha = 0, la_ = 0, hb_ = 0, lb_ = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            ha = dot4(xa.hi[k], 0x01010101u, ha);
-            la_ = dot4(xa.lo[k], 0x01010101u, la_);
-            hb_ = dot4(xb.hi[k], 0x01010101u, hb_);
-            lb_ = dot4(xb.lo[k], 0x01010101u, lb_);
-        }
-        xa.hsum = ha * 256 + la_;
-        xb.hsum = hb_ * 256 + lb_;
+        plane_sums(xa);
+        plane_sums(xb);
     }
     if (!live) {
         xa.scale = xb.scale = 0.f;
@@ -901,7 +939,8 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     const uint32_t cus = 256 * wgs_per_cu - (tail ? 1 : 0);
     const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
     const uint32_t step_rows = 64 / (4 * SLOTS);
-    uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
+    if (set_waves > (uint32_t)gd_threads<ENC>() / 64) return hipErrorInvalidValue;
+    uint32_t sets = (gd_threads<ENC>() / 64) / set_waves;
     // Fewer wave sets for small matrices, so the grid still covers the CUs
     // and each wave streams at least two steps: Q8_0 4096 x 4096 (16 rows
     // per workgroup) took 6.1 us with four sets of one step and 5.5 us with
@@ -960,7 +999,8 @@ static hipError_t launch_dma_segments(hipStream_t s, uint32_t count, const uint8
     }
     const uint32_t set_waves = (nblocks + SLOTS - 1) / SLOTS;
     const uint32_t step_rows = 64 / (4 * SLOTS);
-    uint32_t sets = (GI_WG_THREADS / 64) / set_waves;
+    if (set_waves > (uint32_t)gd_threads<ENC>() / 64) return hipErrorInvalidValue;
+    uint32_t sets = (gd_threads<ENC>() / 64) / set_waves;
     sets = std::min(sets, std::max(1u, (uint32_t)(total / (2 * cus * step_rows))));  // as in launch_dma
     auto lds_for = [&](uint32_t st) {
         const size_t wv = (size_t)set_waves * st;

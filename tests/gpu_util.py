@@ -6,9 +6,9 @@ Tolerances (stated where they are used):
     |gpu - ref| <= 4e-6 * sum|w*x| + 1e-6 per output, the reference's bound
     for its matvecs (metal-check.zig:3976), and normwise
     max|gpu - ref| / max|ref| <= 2e-3 (the stated max relative error);
-  * integer-dot GEMV (activations rounded to 16 bits of their 32-value
-    slice maximum before the exact integer dot): the F32 bound plus the
-    rigorous rounding term sum_c |w[r,c]| * max|x slice(c)| / 65278;
+  * the integer-dot decode GEMV holds the same F32 bound: it carries x as
+    24-bit fixed point per 32-value slice (as many bits as an F32
+    mantissa) into an exact integer dot, with no extra term;
   * f16 MFMA tiles (verify, 128x128 and prefill): weights (and F32
     activations) are rounded to f16, so each term carries at most 2^-11
     relative error per rounded operand; the bound is the reference's own for
@@ -36,14 +36,6 @@ def mass(encoding, w_bytes, rows, columns, x):
     """sum_c |w[r,c] * x[t,c]| for every token t and row r (F64)."""
     dec = orc.decode_matrix(encoding, w_bytes, rows, columns).astype(np.float64)
     return np.abs(np.atleast_2d(x).astype(np.float64)) @ np.abs(dec).T
-
-
-def xq_mass(encoding, w_bytes, rows, columns, x):
-    """sum_c |w[r,c]| * max|x over c's 32-column slice| / 65278 (F64)."""
-    dec = orc.decode_matrix(encoding, w_bytes, rows, columns).astype(np.float64)
-    xs = np.atleast_2d(x).astype(np.float64)
-    amax = np.repeat(np.abs(xs).reshape(xs.shape[0], -1, 32).max(-1), 32, axis=1)
-    return (amax / 65278.0) @ np.abs(dec).T
 
 
 F32_K = 4e-6   # F32 arithmetic (metal-check.zig:3976)

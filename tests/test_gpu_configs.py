@@ -21,7 +21,7 @@ import pytest
 import nuclis_amd as nq
 from nuclis_amd.synth import CONFIGS, X_SEED_GEMV, X_SEED_PREFILL, X_SEED_VERIFY, gaussian
 from oracle import oracle as orc
-from tests.gpu_util import F16_K, F32_K, check_close, mass, to_gpu, xq_mass
+from tests.gpu_util import F16_K, F32_K, check_close, mass, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -53,8 +53,7 @@ def test_config_gemv(backend, name):
     backend.matvec(nq.Matrix(enc, rows, cols, to_gpu(w)), to_gpu(x), out)
     backend.sync()
     want = orc.matvec(enc, rows, cols, w, x)
-    check_close(out.cpu().numpy(), want, mass(enc, w, rows, cols, x)[0], F32_K, f"gemv {name}",
-                extra=xq_mass(enc, w, rows, cols, x)[0])
+    check_close(out.cpu().numpy(), want, mass(enc, w, rows, cols, x)[0], F32_K, f"gemv {name}")
 
 
 @pytest.mark.parametrize("kernel", ["rows", "tile"])

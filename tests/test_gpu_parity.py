@@ -13,12 +13,11 @@ import pytest
 import nuclis_amd as nq
 from nuclis_amd.synth import gaussian
 from oracle import oracle as orc
-from tests.gpu_util import F16_K, F32_K, check_close, mass, to_gpu, xq_mass
+from tests.gpu_util import F16_K, F32_K, check_close, mass, to_gpu
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "decoder_fixtures.json").read_text())
-INT_GEMV = {8, 12, 13, 14, 23}  # encodings whose M=1 GEMV runs on the integer-dot kernels
 
 
 @pytest.fixture(scope="module")
@@ -145,8 +144,7 @@ def test_matvec_matches_oracle(backend, encoding, rows, columns):
     backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
     backend.sync()
     want = orc.matvec(encoding, rows, columns, w, x)
-    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"matvec {encoding}",
-                extra=xq_mass(encoding, w, rows, columns, x)[0] if encoding in INT_GEMV else 0.0)
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"matvec {encoding}")
 
 
 @pytest.mark.parametrize("encoding", ALL)
@@ -163,7 +161,7 @@ def test_matvec_tiled_fixture_blocks_and_basis_columns(backend, encoding):
     backend.matvec(m, to_gpu(x), out)
     backend.sync()
     check_close(out.cpu().numpy(), orc.matvec(encoding, rows, columns, w, x), mass(encoding, w, rows, columns, x)[0],
-                F32_K, "tiled", extra=xq_mass(encoding, w, rows, columns, x)[0] if encoding in INT_GEMV else 0.0)
+                F32_K, "tiled")
     dec = orc.decode_matrix(encoding, w, rows, columns)
     for column in (0, columns // 2 + 1, columns - 1):
         e = np.zeros(columns, np.float32)
@@ -440,8 +438,8 @@ def test_silu_pair_large_runs_as_two_gemvs(backend, rows):
     g = orc.matvec(12, rows, columns, gate, x).astype(np.float64)
     u = orc.matvec(12, rows, columns, up, x).astype(np.float64)
     want = g / (1 + np.exp(-g)) * u
-    eg = F32_K * mass(12, gate, rows, columns, x)[0] + xq_mass(12, gate, rows, columns, x)[0] + 1e-6
-    eu = F32_K * mass(12, up, rows, columns, x)[0] + xq_mass(12, up, rows, columns, x)[0] + 1e-6
+    eg = F32_K * mass(12, gate, rows, columns, x)[0] + 1e-6
+    eu = F32_K * mass(12, up, rows, columns, x)[0] + 1e-6
     bound = 1.1 * np.abs(u) * eg + (np.abs(g) + eg) * eu + 1e-6 * np.abs(want) + 1e-6
     assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
 
@@ -474,7 +472,7 @@ def test_segments_one_encoding_run_as_one_gemv(backend, encoding, columns, rows)
         got = o.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), one.cpu().numpy().view(np.uint32))
         want = orc.matvec(encoding, r, columns, w, x).astype(np.float64)
-        bound = F32_K * mass(encoding, w, r, columns, x)[0] + xq_mass(encoding, w, r, columns, x)[0] + 1e-6
+        bound = F32_K * mass(encoding, w, r, columns, x)[0] + 1e-6
         assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
 
 
@@ -574,3 +572,36 @@ def test_stream_change_orders_work():
             assert torch.equal(outs[i], ref)
     finally:
         b.close()
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 13, 14, 23])
+def test_matvec_wide_range_activations(backend, encoding):
+    """Activations spread over twelve binary decades inside every 32-value
+    slice (the decode GEMV's fixed-point slices are scaled by the slice
+    maximum): the plain F32 bound still holds, as it does for an F32 FMA
+    chain, whose accumulator carries the large terms the same way."""
+    import torch
+    rows, columns = 1024, 5120
+    w = quantized(encoding, rows, columns, 90)
+    rng = np.random.default_rng(91)
+    x = (gaussian(92, columns) * np.exp2(rng.uniform(-6, 6, columns))).astype(np.float32)
+    out = torch.full((rows,), np.nan, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    want = orc.matvec(encoding, rows, columns, w, x)
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, x)[0], F32_K, f"widerange {encoding}")
+
+
+@pytest.mark.parametrize("encoding", [8, 12, 14])
+def test_matvec_nan_activation_poisons_rows(backend, encoding):
+    """A NaN activation makes every output NaN, as in the oracle's F64 sum."""
+    import torch
+    rows, columns = 256, 5120
+    w = quantized(encoding, rows, columns, 93)
+    x = gaussian(94, columns)
+    x[1234] = np.nan
+    out = torch.zeros(rows, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    assert np.isnan(orc.matvec(encoding, rows, columns, w, x)).all()
+    assert np.isnan(out.cpu().numpy()).all()
