@@ -145,6 +145,21 @@ int nuq_matmul_kernel(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, co
 int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x,
                         uint32_t mode);
 
+/* Largest SiLU pair (rows) nuq_matvec_segments_noalloc takes. */
+#define NUQ_NOALLOC_MAX_PAIR_ROWS (1u << 20)
+/* nuq_matvec_segments without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops). The SiLU pair's second GEMV goes to a
+ * fixed 4 MiB scratch array in device memory, one per GPU, held until the
+ * process ends, instead of the context workspace; pairs of more than
+ * NUQ_NOALLOC_MAX_PAIR_ROWS rows are refused (NUQ_INVALID_SHAPE) before
+ * anything is launched. Same validation, kernels and results as
+ * nuq_matvec_segments otherwise. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other contexts of
+ * the same process) race; calls in one stream are ordered. */
+int nuq_matvec_segments_noalloc(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x,
+                                uint32_t mode);
+
 /* Greedy argmax over `count` device logits (sampling/root.zig:226-239: first
  * maximum wins; a non-finite logit gives NUQ_NON_FINITE). `index` is a host
  * pointer; the call synchronizes the context's stream. */

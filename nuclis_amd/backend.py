@@ -27,6 +27,7 @@ Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 12, 13, 14, 23
 F32, F16 = 0, 1
 KERNEL_AUTO, KERNEL_ROWS, KERNEL_TILE, KERNEL_GENERIC = 0, 1, 2, 3
 SEGMENT_PLAIN, SEGMENT_SILU_MUL_PAIR = 0, 1
+NOALLOC_MAX_PAIR_ROWS = 1 << 20  # NUQ_NOALLOC_MAX_PAIR_ROWS (include/nuq.h)
 
 # inference/src/tensor/encoding.zig:29-41: id -> (values per block, bytes per block)
 LAYOUT = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136)}
@@ -109,6 +110,7 @@ EXPORTS = [
     "nuq_validate_row", "nuq_embed", "nuq_dequant_range", "nuq_matvec", "nuq_matvec_rows", "nuq_matmul",
     "nuq_matmul_kernel", "nuq_matvec_segments", "nuq_argmax", "nuq_quantize_rows", "nuq_dequant_rows", "nuq_gemv",
     "nuq_gemm", "nuq_topk", "nuq_penalize", "nuq_reserve_workspace", "nuq_workspace_bytes",
+    "nuq_matvec_segments_noalloc",
 ]
 
 
@@ -146,6 +148,7 @@ def lib() -> ctypes.CDLL:
         L.nuq_matmul.argtypes = [vp, mp, vp, u32, u64, vp, u64, u32]
         L.nuq_matmul_kernel.argtypes = [vp, u32, mp, vp, u32, u64, vp, u64, u32]
         L.nuq_matvec_segments.argtypes = [vp, ctypes.POINTER(_Segment), u32, vp, u32]
+        L.nuq_matvec_segments_noalloc.argtypes = [vp, ctypes.POINTER(_Segment), u32, vp, u32]
         L.nuq_argmax.argtypes = [vp, vp, u64, ctypes.POINTER(u32)]
         L.nuq_quantize_rows.argtypes = [u32, vp, u64, u64, vp, u64]
         _lib = L
@@ -294,6 +297,17 @@ class Backend:
             arr[i].matrix = mat.c()
             arr[i].output = _ptr(out)
         self._call(lib().nuq_matvec_segments, arr, len(segments), _ptr(input), mode)
+
+    def matvec_segments_noalloc(self, segments: list[tuple[Matrix, object]], input, mode: int = SEGMENT_PLAIN) -> None:
+        """matvec_segments without any device allocation (no counterpart in
+        the reference): the SiLU pair's second GEMV uses a fixed per-GPU
+        scratch of NUQ_NOALLOC_MAX_PAIR_ROWS floats; calls that overlap on
+        one GPU race on it."""
+        arr = (_Segment * max(1, len(segments)))()
+        for i, (mat, out) in enumerate(segments):
+            arr[i].matrix = mat.c()
+            arr[i].output = _ptr(out)
+        self._call(lib().nuq_matvec_segments_noalloc, arr, len(segments), _ptr(input), mode)
 
     def penalize(self, logits, history_words, repetition: float, presence: float, count: int | None = None) -> None:
         """Backend.penalize (backends/metal/ops/sampling.zig:58-71), in place.

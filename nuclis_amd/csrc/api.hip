@@ -41,7 +41,16 @@ struct nuq_context {
     nuq::SplitScratch split{nullptr, 0};
     uint64_t *topk_keys = nullptr;  // partial top-k keys between passes
     hipEvent_t handoff = nullptr;   // orders work across a stream change
+    float *static_scratch = nullptr;  // this device's copy of `scratch` (below)
 };
+
+// Scratch of the allocation-free entry point (nuq_matvec_segments_noalloc):
+// the SiLU pair's second GEMV output. One copy per GPU, alive until the
+// process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (nuq_create keeps it in
+// the context), never through the array's name.
+constexpr uint64_t NOALLOC_SCRATCH_FLOATS = NUQ_NOALLOC_MAX_PAIR_ROWS;  // 4 MiB
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
 
 namespace {
 
@@ -263,6 +272,14 @@ nuq_context *nuq_create(int device, char *err, size_t cap) {
     }
     auto *ctx = new nuq_context();
     ctx->device = device;
+    // this device's copy of the allocation-free scratch (device current)
+    if (hipGetSymbolAddress((void **)&ctx->static_scratch, HIP_SYMBOL(scratch)) != hipSuccess ||
+        !ctx->static_scratch) {
+        (void)hipGetLastError();
+        report("hipGetSymbolAddress of the allocation-free scratch failed");
+        delete ctx;
+        return nullptr;
+    }
     if (hipMalloc((void **)&ctx->argmax_buf, 2 * sizeof(uint32_t)) != hipSuccess) {
         report("hipMalloc of the argmax result failed");
         delete ctx;
@@ -449,7 +466,12 @@ int nuq_gemm(nuq_context *ctx, uint32_t encoding, const void *w, uint64_t stride
 // Rows from which a SiLU pair runs as two decode GEMVs plus the epilogue.
 constexpr uint64_t PAIR_SPLIT_ROWS = 4096;
 
-int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode) {
+// The body of both segment entry points. `fixed` (the allocation-free form)
+// is a device buffer of `fixed_floats` floats that takes the SiLU pair's
+// second GEMV instead of the context workspace; the form then never
+// allocates and refuses pairs it cannot hold.
+static int segments_impl(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode,
+                         float *fixed, uint64_t fixed_floats) {
     if (!ctx) return NUQ_INVALID_ARGUMENT;
     if (!segments || count == 0 || count > 4) return fail(ctx, NUQ_INVALID_SHAPE, "segments: 1..4 projections");
     if (mode > NUQ_SEGMENT_SILU_MUL_PAIR) return fail(ctx, NUQ_INVALID_ARGUMENT, "unknown segment mode");
@@ -496,14 +518,17 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
         waves += (uint32_t)((m.rows + rpw - 1) / rpw);
     }
     args.wave_start[count] = waves;
+    if (fixed && mode == NUQ_SEGMENT_SILU_MUL_PAIR && segments[0].matrix.rows > fixed_floats)
+        return fail(ctx, NUQ_INVALID_SHAPE,
+                    "SiLU pair of %llu rows exceeds the allocation-free scratch (at most %llu rows)",
+                    (unsigned long long)segments[0].matrix.rows, (unsigned long long)fixed_floats);
     // A large SiLU pair streams faster as decode GEMVs (gate into the output,
-    // up into the prefill workspace, which no GEMV uses) and the elementwise
-    // epilogue than as one merged row-per-wave pass.
-    const bool pair_split = mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only &&
-                            segments[0].matrix.rows >= PAIR_SPLIT_ROWS &&
-                            ensure_workspace(ctx, segments[0].matrix.rows) &&
-                            segments[0].matrix.rows * sizeof(float) <=
-                                (uint64_t)ctx->split.tiles * 256 * 256 * sizeof(float);
+    // up into a workspace) and the elementwise epilogue than as one merged
+    // row-per-wave pass.
+    const bool pair_big = mode == NUQ_SEGMENT_SILU_MUL_PAIR && !ctx->generic_only &&
+                          segments[0].matrix.rows >= PAIR_SPLIT_ROWS;
+    const bool pair_split = pair_big && (fixed || ensure_workspace(ctx, segments[0].matrix.rows));
+    float *up_buffer = fixed ? fixed : ctx->split.work;
     // Segments of one encoding and row stride (q/k/v, gate/up) run as one
     // launch of the decode GEMV, each matrix on its share of the workgroups.
     bool same = !ctx->generic_only && (mode == NUQ_SEGMENT_PLAIN || pair_split);
@@ -518,19 +543,19 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
             rs[i] = (uint32_t)segments[i].matrix.rows;
             ys[i] = segments[i].output;
         }
-        if (mode != NUQ_SEGMENT_PLAIN) ys[1] = ctx->split.work;
+        if (mode != NUQ_SEGMENT_PLAIN) ys[1] = up_buffer;
         const hipError_t he = nuq::launch_gemv_dma_segments(ctx->stream, segments[0].matrix.encoding, count, ws,
                                                             strides[0], rs, (uint32_t)columns, x, ys);
         if (he != hipErrorInvalidValue) {
             int e = hip_check(ctx, he, "segments gemv launch");
             if (e || mode == NUQ_SEGMENT_PLAIN) return e;
-            return hip_check(ctx, nuq::launch_silu_mul(ctx->stream, segments[0].output, ctx->split.work, rs[0]),
+            return hip_check(ctx, nuq::launch_silu_mul(ctx->stream, segments[0].output, up_buffer, rs[0]),
                              "silu pair epilogue");
         }
     }
     if (pair_split) {
         const nuq_matrix &g = segments[0].matrix, &u = segments[1].matrix;
-        float *up = ctx->split.work;
+        float *up = up_buffer;
         int e = run_gemv(ctx, &g, g.byte_len / g.rows, x, segments[0].output);
         if (e) return e;
         e = run_gemv(ctx, &u, u.byte_len / u.rows, x, up);
@@ -540,6 +565,16 @@ int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t 
     }
     if (mode != NUQ_SEGMENT_PLAIN) args.wave_start[1] = (uint32_t)((segments[0].matrix.rows + rpw - 1) / rpw);
     return hip_check(ctx, nuq::launch_segments(ctx->stream, args, x), "segments launch");
+}
+
+int nuq_matvec_segments(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x, uint32_t mode) {
+    return segments_impl(ctx, segments, count, x, mode, nullptr, 0);
+}
+
+int nuq_matvec_segments_noalloc(nuq_context *ctx, const nuq_segment *segments, uint32_t count, const float *x,
+                                uint32_t mode) {
+    if (!ctx) return NUQ_INVALID_ARGUMENT;
+    return segments_impl(ctx, segments, count, x, mode, ctx->static_scratch, NOALLOC_SCRATCH_FLOATS);
 }
 
 int nuq_argmax(nuq_context *ctx, const float *logits, uint64_t count, uint32_t *index) {
