@@ -233,14 +233,14 @@ def check_gemv(orc, g, encoding, rows, columns, stride_rows=97):
 
 
 def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps=20, warmup=3, w_seed=2,
-               x_seed=5, kernel=None, check=None):
+               x_seed=5, kernel=None, check=None, x_f16=True):
     """`reps` launches of the matmul entry point (one kernel route) on
     rotating weight copies (>= 512 MB), f16 activations; HIP events on the
     launch stream. `check` = (orc, token sample): the timed output is
     compared with the oracle on every row of those tokens."""
     from nuclis_amd.synth import gaussian
     w = nq.quantize(encoding, gaussian(w_seed, (rows, columns), 0.02))
-    xh = gaussian(x_seed, (tokens, columns)).astype(np.float16)
+    xh = gaussian(x_seed, (tokens, columns)).astype(np.float16 if x_f16 else np.float32)
     x = torch.from_numpy(xh).cuda()
     wg = torch.from_numpy(w).cuda()
     mats = [nq.Matrix(encoding, rows, columns, wg if i == 0 else wg.clone()) for i in range(copies_for(w.nbytes))]
@@ -423,6 +423,12 @@ def main():
                                kernel=kid, check=(orc, np.arange(8), 4e-6 if kname == "rows" else 2e-4))
                 d["algo_gbs"] = (rr * cc // 256 * 144 + 8 * cc * 2 + 8 * rr * 4) / d["ms"] / 1e6
                 configs[f"configs[3] verify M=8 q4_k {label} {kname}"] = d
+        # the routed multi-token GEMV (T = 2, 3 F32 token rows, matvecRows)
+        for tokens in (2, 3):
+            d = bench_gemm(torch, nq, backend, stream, e, r, c, tokens, reps=200, warmup=20, w_seed=sd, x_seed=4,
+                           kernel=nq.KERNEL_AUTO, x_f16=False, check=(orc, np.arange(tokens), 4e-6))
+            d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]
+            configs[f"multi-token T={tokens} f32 q4_k gate 17408x5120 (auto route)"] = d
     prefill = None
     if want("prefill"):
         e, r, c, sd = CONFIGS["c5_gate"]

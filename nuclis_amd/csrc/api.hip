@@ -189,6 +189,20 @@ int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float
                      "gemv launch");
 }
 
+// F32 activations of 2..3 tokens at F32 precision on the matrix cores
+// (Q4_K / Q5_K); returns -1 when the shape is not one it takes.
+int run_rows_mfma(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, uint64_t in_stride,
+                  float *out, uint64_t out_stride, uint32_t tokens) {
+    if (tokens < 2 || tokens > 3 || (m->encoding != NUQ_Q4_K && m->encoding != NUQ_Q5_K)) return -1;
+    (void)ensure_workspace(ctx, nuq::tile_workspace_floats(m->encoding, (uint32_t)m->rows, (uint32_t)m->columns,
+                                                           tokens, in_stride, true));
+    const hipError_t e = nuq::launch_rows_mfma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
+                                               (uint32_t)m->rows, (uint32_t)m->columns, x, in_stride, out, out_stride,
+                                               tokens, ctx->split);
+    if (e == hipErrorInvalidValue) return -1;
+    return hip_check(ctx, e, "multi-token gemv launch");
+}
+
 int run_generic(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const void *x, uint32_t x_f16,
                 uint64_t in_stride, float *out, uint64_t out_stride, uint32_t tokens) {
     return hip_check(ctx,
@@ -222,6 +236,10 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_AUTO) {
         if (tokens == 1 && !f16) return run_gemv(ctx, m, stride, (const float *)x, out);
+        if (!f16) {
+            const int r = run_rows_mfma(ctx, m, stride, (const float *)x, in_stride, out, out_stride, tokens);
+            if (r >= 0) return r;
+        }
         kernel = tokens <= 3 && specialised(m->encoding) ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
     }
     if (kernel == NUQ_KERNEL_ROWS && !specialised(m->encoding))
@@ -407,8 +425,11 @@ int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint6
     if (!x || !out) return fail(ctx, NUQ_INVALID_ARGUMENT, "null input or output");
     if ((uintptr_t)x % 16 != 0 || in_stride % 4 != 0 || (uintptr_t)out % 4 != 0)
         return fail(ctx, NUQ_INVALID_SHAPE, "input must be float4 aligned (offset and stride)");
-    if (ctx->generic_only || !vector_aligned(m, stride, x) || !specialised(m->encoding))
+    if (ctx->generic_only || !vector_aligned(m, stride, x))
         return run_generic(ctx, m, stride, x, 0, in_stride, out, out_stride, tokens);
+    const int r = run_rows_mfma(ctx, m, stride, x, in_stride, out, out_stride, tokens);
+    if (r >= 0) return r;
+    if (!specialised(m->encoding)) return run_generic(ctx, m, stride, x, 0, in_stride, out, out_stride, tokens);
     return hip_check(ctx,
                      nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
                                       (uint32_t)m->columns, x, 0, in_stride, out, out_stride, tokens),

@@ -1442,9 +1442,12 @@ __device__ __forceinline__ void vd_ring_read(uint32_t a, uint32_t c, uint4 (&hd)
 // The arithmetic of one streamed-verify step over NL live blocks: per
 // block an independent chain of eight f16 MFMAs against q * sc, scaled by
 // the block's d, plus one chain of F32 MFMAs for the minimum terms.
-template <typename L, uint32_t NB, uint32_t NL>
+// With XS = 3 each D row m is one f16 part of a token's activations scaled
+// by a power of two per (token, block); sfm[s][e] undoes it for D row 4h+e.
+template <typename L, uint32_t NB, uint32_t NL, uint32_t XS>
 __device__ __forceinline__ floatx4 vd_step_blocks(const uint4 (&hd)[NB][L::NH], const uint4 (&cq)[NB][2], uint32_t h,
-                                                  const half8 (&bx)[NB][8], const float (&sx)[NB][2]) {
+                                                  const half8 (&bx)[NB][8], const float (&sx)[NB][2],
+                                                  const float (&sfm)[NB][4]) {
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     floatx4 part[NL], accm = zero;
     float d[NL];
@@ -1463,7 +1466,7 @@ __device__ __forceinline__ floatx4 vd_step_blocks(const uint4 (&hd)[NB][L::NH], 
 #pragma unroll
     for (uint32_t s = 0; s < NL; ++s)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = fmaf(d[s], part[s][e], acc[e]);
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(XS == 3 ? d[s] * sfm[s][e] : d[s], part[s][e], acc[e]);
     return acc;
 }
 
@@ -1496,7 +1499,43 @@ __device__ __forceinline__ void vd_read_x(uint32_t a, u32x4 (&r)[8]) {
         : "memory");
 }
 
-template <uint32_t ENC, uint32_t NB, typename XT, int STAGE, uint32_t DEPTH>
+// Cross-lane reductions on the VALU (DPP within a 16-lane row, the gfx950
+// row swaps across rows), no LDS round trips. Every lane ends with the same
+// bits, added in the same order.
+template <int CTRL>
+__device__ __forceinline__ float vd_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// sum over the four rows: lanes l, l ^ 16, l ^ 32, l ^ 48
+__device__ __forceinline__ float vd_rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// maximum over the whole wave
+__device__ __forceinline__ float vd_wave_max(float v) {
+    v = fmaxf(v, vd_dpp<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, vd_dpp<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, vd_dpp<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, vd_dpp<0x140>(v));  // row_mirror
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// XS = 3 (F32 activations, at most 3 tokens): A row 4p + t is part p of
+// token t's activations, x * 2^e = p0 + p1 + p2 (each part the f16 rounding
+// of what the earlier ones leave, so the sum holds every bit of x), with
+// 2^e per (token, wave run) putting the run's largest |x| in [2^14, 2^15).
+// The weights are exact f16 integers, so every product is exact and the
+// MFMA sums carry F32 rounding only: the F32 precision of the multi-token
+// GEMV (ops/matvec.zig:149-188) on the matrix cores. A lane's D rows 4h + e
+// are part h of token e, so adding the four h lanes gives the token's sum;
+// the partial sums then hold 4 tokens per (row, wave). The parts are staged
+// per wave (STAGE 1), part p of token t at staging row pT + t.
+template <uint32_t ENC, uint32_t NB, typename XT, int STAGE, uint32_t DEPTH, uint32_t XS = 1>
 __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(const uint8_t *__restrict__ w_all,
                                                                         uint64_t stride, uint32_t rows,
                                                                         uint32_t nblocks_all,
@@ -1562,6 +1601,8 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         }                                                                                               \
     }
     half8 bx[NB][8];
+    float sx3[NB][2], sft[4];  // XS = 3: F32 group sums; each token's scale back
+    float gs3[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // XS = 3: staged group sums of this lane's token
     if constexpr (STAGE != 0) {
         // this wave's activations, [token][its blocks' 512 bytes], copied
         // before the step-0 weights so that they are waited for alone
@@ -1569,24 +1610,123 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
         const uint32_t span_log2 = nlive == 2 ? 6 : 5;  // log2(span / 16)
         uint8_t *xs = STAGE == 1 ? ring + V::SLOT : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
-        for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
-            const uint32_t k = 64 * jx + lane;
-            if (k < xchunks) {
-                const uint32_t t = k >> span_log2, rem = k & ((1u << span_log2) - 1);
-                const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
-                __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(xs + 1024 * jx), 16, 0, 0);
+        if constexpr (XS == 3) {
+            // F32 activations: lane k converts values [8k, 8k + 8) of the
+            // wave's run of each token into its three f16 parts (staging
+            // rows pT + t), the F32 sums of 32-value groups go to the lanes
+            // that need them, and the wave agrees on the token's scale 2^e
+            static_assert(STAGE == 1, "F32 activations are staged in the wave's own region");
+            NUQ_VD_DMA(0, 0)
+            (void)xchunks;
+            (void)span_log2;
+            // (LDS accesses as asm: see vd_read_x)
+            const bool live_k = 8 * lane < nlive * 256;
+            // every token's values are loaded before the step-0 copies; lanes
+            // past the run and tokens past `tokens` load valid bytes and drop them
+            float4 fl[3][2];
+#pragma unroll
+            for (uint32_t t = 0; t < 3; ++t) {
+                const float *src = (const float *)x + (uint64_t)min(t, tokens - 1) * in_stride + b0 * L::BLOCK_VALUES +
+                                   8 * (live_k ? lane : 0);
+                fl[t][0] = *(const float4 *)src;
+                fl[t][1] = *(const float4 *)(src + 4);
             }
+            NUQ_VD_DMA(0, 0)
+#pragma unroll
+            for (uint32_t t = 0; t < 4; ++t) sft[t] = 0.f;
+#pragma unroll
+            for (uint32_t t = 0; t < 3; ++t) {
+                if (t >= tokens) continue;
+                const float f[8] = {fl[t][0].x, fl[t][0].y, fl[t][0].z, fl[t][0].w,
+                                    fl[t][1].x, fl[t][1].y, fl[t][1].z, fl[t][1].w};
+                float amax = 0.f, cs = 0.f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    amax = fmaxf(amax, fabsf(f[k]));
+                    cs += f[k];
+                }
+                if (!live_k) amax = cs = 0.f;
+                amax = vd_wave_max(amax);
+                // group sums: the four lanes of a 32-value group
+                cs += vd_dpp<0xb1>(cs);
+                cs += vd_dpp<0x4e>(cs);
+                // lane (r16, h) of part 0 of this token keeps the sums of
+                // groups 2h, 2h + 1 of each block: lanes 32s + 8h + 4q
+#pragma unroll
+                for (uint32_t sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (uint32_t q = 0; q < 2; ++q) {
+                        const float g = __shfl(cs, 32 * sb + 8 * h + 4 * q, 64);
+                        if ((r16 & 3) == t) gs3[sb][q] = g;
+                    }
+                // 2^e with the run's largest |x| * 2^e in [2^14, 2^15); 1 for
+                // zero or non-finite runs (non-finite values reach the MFMA)
+                int ex = 0;
+                if (amax > 0.f && amax <= 3.0e38f) {
+                    (void)frexpf(amax, &ex);
+                    ex = 15 - ex;
+                }
+                sft[t] = ldexpf(1.f, -ex);
+                half8 p0, p1, p2;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float xv = ldexpf(f[k], ex);
+                    p0[k] = (_Float16)xv;
+                    const float r1 = xv - (float)p0[k];
+                    p1[k] = (_Float16)r1;
+                    p2[k] = (_Float16)(r1 - (float)p1[k]);
+                }
+                if (live_k) {
+                    uint32_t dst = vd_lds_addr(xs + t * span + 16 * lane);
+                    const uint32_t pst = tokens * span;
+                    asm volatile("ds_write_b128 %0, %1\n\t"
+                                 "v_add_u32 %0, %0, %4\n\t"
+                                 "ds_write_b128 %0, %2\n\t"
+                                 "v_add_u32 %0, %0, %4\n\t"
+                                 "ds_write_b128 %0, %3"
+                                 : "+&v"(dst)
+                                 : "v"(__builtin_bit_cast(u32x4, p0)), "v"(__builtin_bit_cast(u32x4, p1)),
+                                   "v"(__builtin_bit_cast(u32x4, p2)), "v"(pst)
+                                 : "memory");
+                }
+            }
+        } else {
+            for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
+                const uint32_t k = 64 * jx + lane;
+                if (k < xchunks) {
+                    const uint32_t t = k >> span_log2, rem = k & ((1u << span_log2) - 1);
+                    const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
+                    __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(xs + 1024 * jx), 16, 0, 0);
+                }
+            }
+            NUQ_VD_DMA(0, 0)
         }
-        NUQ_VD_DMA(0, 0)
         asm volatile("s_waitcnt vmcnt(%0)" : : "n"(V::INSTRS) : "memory");
         // lanes of tokens past `tokens` read token 0: they reach only D rows
-        // that are never stored
-        const uint32_t xa = vd_lds_addr(xs) + (r16 < tokens ? r16 : 0) * span + 128 * h;
+        // that are never stored. XS = 3: A row r16 = 4p + t is part p of
+        // token t; rows of p = 3 or t >= tokens are zero (they are added
+        // into the stored sums).
+        const uint32_t ap = r16 >> 2, at = r16 & 3;
+        const bool arow = XS == 3 ? ap < 3 && at < tokens : r16 < tokens;
         u32x4 xr[NB][8] = {};  // a wave's block past the row's end stays zero
-        vd_read_x<0>(xa, xr[0]);
-        if (nlive > 1) vd_read_x<512>(xa, xr[1]);
-        if constexpr (NB > 2) {
-            if (nlive > 2) vd_read_x<1024>(xa, xr[2]);
+        {
+            // XS = 3: staging row pT + t
+            const uint32_t srow = XS == 3 ? (arow ? ap * tokens + at : 0) : (arow ? r16 : 0);
+            const uint32_t xa = vd_lds_addr(xs) + srow * span + 128 * h;
+            vd_read_x<0>(xa, xr[0]);
+            if (nlive > 1) vd_read_x<512>(xa, xr[1]);
+            if constexpr (NB > 2) {
+                if (nlive > 2) vd_read_x<1024>(xa, xr[2]);
+            }
+        }
+        if constexpr (XS == 3) {
+            // F32 group sums 2h, 2h + 1 of each block, for part 0 of a token
+#pragma unroll
+            for (uint32_t s = 0; s < NB; ++s) {
+                const bool ok = arow && ap == 0 && s < nlive;
+                sx3[s][0] = ok ? gs3[s][0] : 0.f;
+                sx3[s][1] = ok ? gs3[s][1] : 0.f;
+            }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
 #pragma unroll
@@ -1594,6 +1734,7 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 asm volatile("" : "+v"(xr[s][c]));
+                if (XS == 3 && !arow) xr[s][c] = u32x4{0u, 0u, 0u, 0u};
                 bx[s][c] = __builtin_bit_cast(half8, xr[s][c]);
             }
         // the fragments are in registers: slots 1.. take their first steps
@@ -1639,9 +1780,17 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
 
     // F32 sums of the f16 activations of groups 2h and 2h+1 of each block
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
-    float sx[NB][2];
+    float sx[NB][2], sfm[NB][4];
 #pragma unroll
     for (uint32_t s = 0; s < NB; ++s) {
+        if constexpr (XS == 3) {
+            sx[s][0] = sx3[s][0];
+            sx[s][1] = sx3[s][1];
+            // D row 4h + e is part h of token e
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sfm[s][e] = sft[e];
+            continue;
+        }
         sx[s][0] = sx[s][1] = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -1675,14 +1824,22 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         // one copy of the step body per live block count (wave-uniform), so
         // the per-block results need no merging
         static_assert(NB == 2, "live block counts 1 and 2");
-        const floatx4 acc = nlive == NB ? vd_step_blocks<L, NB, NB>(hd, cq, h, bx, sx)
-                                        : vd_step_blocks<L, NB, 1>(hd, cq, h, bx, sx);
+        const floatx4 acc = nlive == NB ? vd_step_blocks<L, NB, NB, XS>(hd, cq, h, bx, sx, sfm)
+                                        : vd_step_blocks<L, NB, 1, XS>(hd, cq, h, bx, sx, sfm);
         // D: lane holds row base + r16 (base = min(16 i, nrow - 16)), tokens
         // 4h..4h+3; rows an earlier step stored are skipped (written through
         // asm: the compiler would otherwise wait for every ring copy in flight)
         const uint32_t base = min(16 * i, nrow - 16);
-        if (store_tokens && base + r16 >= 16 * i)
+        if constexpr (XS == 3) {
+            // the token's three parts (and the zero rows of h = 3) add up
+            floatx4 sum = acc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[e] = vd_rows_sum(sum[e]);
+            if (h == 0 && base + r16 >= 16 * i)
+                asm volatile("ds_write_b128 %0, %1" : : "v"(part_a + base * (part_step / 16)), "v"(sum) : "memory");
+        } else if (store_tokens && base + r16 >= 16 * i) {
             asm volatile("ds_write_b128 %0, %1" : : "v"(part_a + base * (part_step / 16)), "v"(acc) : "memory");
+        }
     }
 #undef NUQ_VD_DMA
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
@@ -1711,25 +1868,27 @@ static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t
                                        uint32_t nblocks, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                                        uint64_t out_stride, uint32_t tokens, uint32_t tpad, uint32_t wgs,
                                        const VdLayout &L, uint32_t waves, uint32_t ranges, uint32_t kb,
-                                       uint64_t y_range) {
+                                       uint64_t y_range, bool xs3) {
     const dim3 grid(wgs, ranges), block(64 * waves);
-#define NUQ_VD_LAUNCH(XT_, MODE_, D_)                                                                        \
-    hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_, D_>), grid, block, L.lds, s, w, stride, rows,    \
+#define NUQ_VD_LAUNCH(XT_, MODE_, D_, XS_)                                                                   \
+    hipLaunchKernelGGL((verify_dma_kernel<ENC, NB, XT_, MODE_, D_, XS_>), grid, block, L.lds, s, w, stride, rows, \
                        nblocks, (const XT_ *)x, in_stride, y, out_stride, tokens, tpad, L.region, L.slot_gap,      \
                        L.part_off, kb, y_range)
-#define NUQ_VD_LAUNCH_D(XT_, MODE_)                                                                          \
+#define NUQ_VD_LAUNCH_D(XT_, MODE_, XS_)                                                                     \
     if (L.depth == 3)                                                                                       \
-        NUQ_VD_LAUNCH(XT_, MODE_, 3);                                                                       \
+        NUQ_VD_LAUNCH(XT_, MODE_, 3, XS_);                                                                  \
     else                                                                                                    \
-        NUQ_VD_LAUNCH(XT_, MODE_, 2);
-    if (x_f16 && L.stage == 1) {
-        NUQ_VD_LAUNCH_D(_Float16, 1)
+        NUQ_VD_LAUNCH(XT_, MODE_, 2, XS_);
+    if (xs3) {
+        NUQ_VD_LAUNCH_D(float, 1, 3)
+    } else if (x_f16 && L.stage == 1) {
+        NUQ_VD_LAUNCH_D(_Float16, 1, 1)
     } else if (x_f16 && L.stage == 2) {
-        NUQ_VD_LAUNCH_D(_Float16, 2)
+        NUQ_VD_LAUNCH_D(_Float16, 2, 1)
     } else if (x_f16) {
-        NUQ_VD_LAUNCH_D(_Float16, 0)
+        NUQ_VD_LAUNCH_D(_Float16, 0, 1)
     } else {
-        NUQ_VD_LAUNCH_D(float, 0)
+        NUQ_VD_LAUNCH_D(float, 0, 1)
     }
 #undef NUQ_VD_LAUNCH_D
 #undef NUQ_VD_LAUNCH
@@ -1751,22 +1910,29 @@ __global__ void verify_reduce_kernel(const float *__restrict__ ws, uint32_t nran
 // Streams when the row's blocks fit 12 waves of at most 2 blocks, or, with a
 // workspace, in K ranges of at most 24 blocks whose sums verify_reduce_kernel
 // adds; returns false (nothing launched) otherwise.
+// xs3: F32 activations of at most 5 tokens as three f16 parts each (the
+// kernel's XS = 3): F32 precision.
 template <uint32_t ENC>
 static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks_all,
                               const void *x, uint32_t x_f16, uint64_t in_stride, float *y_out,
-                              uint64_t out_stride_out, uint32_t tokens, hipError_t *err,
-                              const SplitScratch *scratch = nullptr) {
+                              uint64_t out_stride_out, uint32_t out_tokens, hipError_t *err,
+                              const SplitScratch *scratch = nullptr, bool xs3 = false) {
+    if (xs3 && (x_f16 || out_tokens > 3)) return false;
+    const uint32_t tokens = out_tokens;
     constexpr uint32_t MAXW = vd_max_waves<2>();
     constexpr size_t LDS = 160 * 1024;
     if (rows < 16) return false;
     // K ranges: longer rows (the down projection) run as `ranges` ranges of
     // kb blocks over the workgroups, into the prefill workspace
     uint32_t ranges = 1, kb = nblocks_all;
-    if (nblocks_all > 2 * MAXW) {
-        ranges = (nblocks_all + 2 * MAXW - 1) / (2 * MAXW);
+    // (xs3: at most 18 blocks per range, so 9 waves' regions hold the
+    // three part rows per token beside the step-0 slot)
+    const uint32_t max_kb = xs3 ? 18 : 2 * MAXW;
+    if (nblocks_all > max_kb) {
+        ranges = (nblocks_all + max_kb - 1) / max_kb;
         kb = (nblocks_all + ranges - 1) / ranges;
         if (!scratch || !scratch->work ||
-            (uint64_t)ranges * tokens * rows > (uint64_t)scratch->tiles * 256 * 256)
+            (uint64_t)ranges * out_tokens * rows > (uint64_t)scratch->tiles * 256 * 256)
             return false;
     }
     const uint32_t nblocks = kb;
@@ -1777,12 +1943,15 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // SIMD (one wave left alone on its SIMD at the end) and than 12 waves of
     // 1 or 2 blocks (5 blocks on every SIMD, but more per-wave overhead).
     const uint32_t waves = (nblocks + 1) / 2;
-    const uint32_t tpad = (tokens + 3) & ~3u;
+    const uint32_t tpad = xs3 ? 4 : (tokens + 3) & ~3u;
     const size_t slot = VDma<ENC, 2>::SLOT;
     // wave kw's run: [kw nblocks / waves, (kw + 1) nblocks / waves)
     uint32_t max_run = 0;
     for (uint32_t k = 0; k < waves; ++k) max_run = std::max(max_run, (k + 1) * nblocks / waves - k * nblocks / waves);
-    const size_t xwave = (size_t)tokens * max_run * 512, xall = (size_t)tokens * nblocks * 512;
+    // staged activations per wave: f16 rows, or (xs3) three part rows per
+    // token
+    const size_t xwave = (size_t)(xs3 ? 3 : 1) * tokens * max_run * 512;
+    const size_t xall = (size_t)tokens * nblocks * 512;
     const size_t per_row = (size_t)waves * tpad * 4;
     // One workgroup per CU when the partial sums of its rows fit, else more,
     // shorter row ranges; never more than rows / 16 workgroups, so each range
@@ -1796,8 +1965,8 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // one holding the most.
     VdLayout L{}, best{};
     uint32_t best_rows = 0;
-    const int modes_f16[3] = {1, 2, 0}, modes_f32[1] = {0};
-    const int *modes = x_f16 ? modes_f16 : modes_f32;
+    const int modes_f16[3] = {1, 2, 0}, modes_f32[1] = {0}, modes_xs3[1] = {1};
+    const int *modes = xs3 ? modes_xs3 : x_f16 ? modes_f16 : modes_f32;
     bool found = false;
     for (uint32_t depth = 3; depth >= 2 && !found; --depth) {
         for (int m = 0; m < (x_f16 ? 3 : 1); ++m) {
@@ -1837,11 +2006,11 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     const size_t xall_lds = L.stage == 2 ? waves * slot + xall : 0;
     L.lds = std::max(rings_end + rows_per_wg * L.per_row, xall_lds);
     *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks_all, x, x_f16, in_stride, y, out_stride, tokens,
-                                        tpad, wgs, L, waves, ranges, kb, (uint64_t)tokens * rows);
+                                        tpad, wgs, L, waves, ranges, kb, (uint64_t)out_tokens * rows, xs3);
     if (*err == hipSuccess && ranges > 1) {
-        const uint32_t n = rows * tokens;
+        const uint32_t n = rows * out_tokens;
         hipLaunchKernelGGL(verify_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, scratch->work, ranges, rows,
-                           tokens, y_out, out_stride_out);
+                           out_tokens, y_out, out_stride_out);
         *err = hipGetLastError();
     }
     return true;
@@ -1907,17 +2076,33 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 }
 
 
+hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                            uint32_t columns, const float *x, uint64_t in_stride, float *y, uint64_t out_stride,
+                            uint32_t tokens, const SplitScratch &scratch) {
+    if (tokens < 1 || tokens > 3 || columns % 256 != 0) return hipErrorInvalidValue;
+    hipError_t err = hipErrorInvalidValue;
+    bool launched = false;
+    if (encoding == 12)
+        launched = launch_verify_dma<12>(s, w, stride, rows, columns / 256, x, 0, in_stride, y, out_stride, tokens,
+                                         &err, &scratch, true);
+    else if (encoding == 13)
+        launched = launch_verify_dma<13>(s, w, stride, rows, columns / 256, x, 0, in_stride, y, out_stride, tokens,
+                                         &err, &scratch, true);
+    return launched ? err : hipErrorInvalidValue;
+}
+
 uint32_t split_scratch_tiles() { return 4 * compute_units(); }
 
 uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t columns, uint32_t tokens,
-                               uint64_t in_stride) {
+                               uint64_t in_stride, bool xs3) {
     if (tokens <= 16 && columns % 256 == 0) {
         // the streamed verify tile's K ranges (Q4_K / Q5_K rows longer than
-        // 2 * MAXW blocks), one F32 partial per range, token and row
+        // 2 * MAXW blocks, or 18 for the F32 multi-token form), one F32
+        // partial per range, token and row
         constexpr uint32_t MAXW = vd_max_waves<2>();
-        const uint32_t nblocks = columns / 256;
-        if ((encoding != 12 && encoding != 13) || nblocks <= 2 * MAXW || rows < 16) return 0;
-        return (uint64_t)((nblocks + 2 * MAXW - 1) / (2 * MAXW)) * tokens * rows;
+        const uint32_t nblocks = columns / 256, max_kb = xs3 ? 18 : 2 * MAXW;
+        if ((encoding != 12 && encoding != 13) || nblocks <= max_kb || rows < 16) return 0;
+        return (uint64_t)((nblocks + max_kb - 1) / max_kb) * tokens * rows;
     }
     if (tokens > 128 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {  // as launch_tile routes
         const uint32_t cus = compute_units();

@@ -77,10 +77,17 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);
 uint32_t split_scratch_tiles();
+// Multi-token GEMV of F32 activations (1..3 tokens) at F32 precision on the
+// matrix cores (the streamed verify tile with each token's activations as
+// three f16 parts); Q4_K / Q5_K. hipErrorInvalidValue (nothing launched)
+// for shapes it does not take.
+hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
+                            uint32_t columns, const float *x, uint64_t in_stride, float *y, uint64_t out_stride,
+                            uint32_t tokens, const SplitScratch &scratch);
 // F32 workspace the tile route of this call would use (verify K ranges or
 // prefill split partials); 0 when it needs none. A smaller workspace makes
 // the route fall back (fewer splits, or the register verify tile).
 uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t columns, uint32_t tokens,
-                               uint64_t in_stride);
+                               uint64_t in_stride, bool xs3 = false);
 
 }  // namespace nuq

@@ -605,3 +605,36 @@ def test_matvec_nan_activation_poisons_rows(backend, encoding):
     backend.sync()
     assert np.isnan(orc.matvec(encoding, rows, columns, w, x)).all()
     assert np.isnan(out.cpu().numpy()).all()
+
+
+# Multi-token GEMV at F32 precision on the matrix cores (Q4_K / Q5_K, 2..3
+# F32 token rows): each token's activations enter the MFMAs as three f16
+# parts holding every bit of x, so the plain F32 bound applies.
+# (From four tokens the f16 tile takes over, as the reference's half tiles
+# do from four tokens, ops/matmul.zig:86-108.)
+MULTI_TOKEN_CASES = [(e, r, c, t) for (e, r, c) in [(12, 17408, 5120), (12, 5120, 17408), (13, 1040, 5120),
+                                                    (12, 40, 1280), (12, 1000, 4608), (13, 520, 17408)]
+                     for t in (2, 3)]
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens", MULTI_TOKEN_CASES)
+def test_multi_token_f32_matches_oracle(backend, encoding, rows, columns, tokens):
+    import torch
+    w = quantized(encoding, rows, columns, 95 + tokens)
+    rng = np.random.default_rng(96 + tokens)
+    x = gaussian(97 + tokens, (tokens, columns))
+    x[-1] *= np.exp2(rng.uniform(-6, 6, columns)).astype(np.float32)  # wide range inside each run
+    in_stride, out_stride = columns + 4, rows + 8
+    xs = np.zeros((tokens, in_stride), np.float32)
+    xs[:, :columns] = x
+    print(f"[multi-token] enc {encoding} {rows}x{columns} T={tokens}", flush=True)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    out = torch.full((tokens, out_stride), np.nan, device="cuda")
+    backend.matmul(m, to_gpu(xs), in_stride, out, out_stride, tokens)
+    out2 = torch.full((tokens, out_stride), np.nan, device="cuda")
+    backend.matvec_rows(m, to_gpu(xs), in_stride, out2, out_stride, tokens)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, x)
+    got = out.cpu().numpy()[:, :rows]
+    check_close(got, want, mass(encoding, w, rows, columns, x), F32_K, f"multitoken {encoding}")
+    assert np.array_equal(got.view(np.uint32), out2.cpu().numpy()[:, :rows].view(np.uint32))
