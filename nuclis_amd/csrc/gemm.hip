@@ -339,48 +339,50 @@ struct WRaw<12> {
         *(half4v_t *)(out + 32 + part * 16 + 4 * c) = pf_four(hi, (_Float16)1024.f, mul1, -off1);
     }
 };
+// Q6_K slabs are not 64 consecutive columns: slab ks of block ks / 4 holds
+// quarters qa and qa + 2 (qa = ks & 1) of half (ks & 3) / 2, the two
+// quarters whose 6-bit codes share their ql bytes (low and high nibbles) and
+// their qh bytes (bits 2qa and 2qa + 4). Part p = values 16p .. 16p + 15 of
+// both quarters (slab columns 16p.. and 32 + 16p..), so a thread loads 16
+// ql bytes, 16 qh bytes, the scales and d once for 32 values.
 template <>
 struct WRaw<14> {
-    uint32_t ql[8], qh[8];
-    uint32_t sc;  // the two int8 scales of this quarter (bytes 0, 1)
+    uint4 ql, qh, sc16;
     uint32_t d16;
-    float mul_a, mul_b;
+    float mul_lo, mul_hi;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(ks >> 2) * 210;
-        const uint32_t h = (ks & 3) >> 1, q = 2 * (ks & 1) + part;
-        const uint8_t *lp = blk + h * 64 + (q & 1) * 32;
-        const uint8_t *hp = blk + 128 + h * 32;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            ql[k] = load_u32_unaligned(lp + 4 * k);
-            qh[k] = load_u32_unaligned(hp + 4 * k);
-        }
-        sc = load_u16_bytes(blk + 192 + h * 8 + 2 * q);
+        const uint32_t h = (ks & 3) >> 1, qa = ks & 1;
+        // 2-byte aligned blocks: unaligned 16-byte loads (ROCm runs global
+        // memory in unaligned mode)
+        typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+        const u32x4_a2 a = *(const u32x4_a2 *)(blk + h * 64 + qa * 32 + 16 * part);
+        const u32x4_a2 b = *(const u32x4_a2 *)(blk + 128 + h * 32 + 16 * part);
+        const u32x4_a2 c = *(const u32x4_a2 *)(blk + 192);
+        ql = make_uint4(a.x, a.y, a.z, a.w);
+        qh = make_uint4(b.x, b.y, b.z, b.w);
+        sc16 = make_uint4(c.x, c.y, c.z, c.w);
         d16 = load_u16_bytes(blk + 208);
     }
     __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
-        const uint32_t q = 2 * (ks & 1) + part;
-        const uint32_t lshift = (q >> 1) * 4, hshift = 2 * q;
+        const uint32_t h = (ks & 3) >> 1, qa = ks & 1;
         if (c == 0) {
+            // scales of values 16 part.. of quarters qa and qa + 2: bytes
+            // idx = 8h + 2qa + part and idx + 4 (dwords 2h and 2h + 1)
             const float d = half_bits(d16);
-            mul_a = d * (float)(int8_t)(sc & 0xff);
-            mul_b = d * (float)(int8_t)(sc >> 8);
+            const uint32_t lo_word = h ? sc16.z : sc16.x, hi_word = h ? sc16.w : sc16.y;
+            const uint32_t sh = 8 * (2 * qa + part);
+            mul_lo = d * (float)(int8_t)((lo_word >> sh) & 0xffu);
+            mul_hi = d * (float)(int8_t)((hi_word >> sh) & 0xffu);
         }
-        const float mul = c < 2 ? mul_a : mul_b;
-        half8 v;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t u = opaque_and<0x0f0f0f0fu>(ql[2 * c + kk] >> lshift) |
-                               opaque_and<0x30303030u>((qh[2 * c + kk] >> hshift) << 4);
-            // mul * (q - 32): the product of the exact f16 integer q - 32
-            // equals the former fma(mul, q, -32 * mul) before rounding
-            const half4v_t f = pf_four(u, (_Float16)1056.f, mul, 0.f);
-            v[kk * 4 + 0] = f[0];
-            v[kk * 4 + 1] = f[1];
-            v[kk * 4 + 2] = f[2];
-            v[kk * 4 + 3] = f[3];
-        }
-        *(half8 *)(out + part * 32 + 8 * c) = v;
+        const uint32_t l = c == 0 ? ql.x : c == 1 ? ql.y : c == 2 ? ql.z : ql.w;
+        const uint32_t hb = c == 0 ? qh.x : c == 1 ? qh.y : c == 2 ? qh.z : qh.w;
+        const uint32_t s0 = 2 * qa;
+        const uint32_t ulo = opaque_and<0x0f0f0f0fu>(l) | (opaque_and<0x03030303u>(hb >> s0) << 4);
+        const uint32_t uhi = opaque_and<0x0f0f0f0fu>(l >> 4) | (opaque_and<0x03030303u>(hb >> (s0 + 4)) << 4);
+        // mul * (u - 32): the product of the exact f16 integer u - 32
+        *(half4v_t *)(out + part * 16 + 4 * c) = pf_four(ulo, (_Float16)1056.f, mul_lo, 0.f);
+        *(half4v_t *)(out + 32 + part * 16 + 4 * c) = pf_four(uhi, (_Float16)1056.f, mul_hi, 0.f);
     }
 };
 template <>
@@ -505,7 +507,19 @@ typedef __attribute__((address_space(1))) void global_void_t;
 // for the whole K loop, so they are computed once (XDma::init) and each
 // slab's copies are a uniform base plus those offsets.
 constexpr uint32_t XD_INSTRS = PF_BM * 9 / 64;  // 36
-template <uint32_t NW>
+
+// First column of K slab ks, and the offset of slab chunk c (8 columns)
+// from it: 64 consecutive columns, except Q6_K (see WRaw<14>), whose slab
+// is two 32-column pieces 64 columns apart.
+template <uint32_t ENC>
+__device__ __forceinline__ uint32_t slab_k0(uint32_t ks) {
+    return ENC == 14 ? (ks >> 2) * 256 + ((ks & 3) >> 1) * 128 + (ks & 1) * 32 : ks * BK;
+}
+template <uint32_t ENC>
+__device__ __forceinline__ uint32_t slab_chunk_col(uint32_t c) {
+    return ENC == 14 && c >= 4 ? 64 + 8 * (c - 4) : 8 * c;
+}
+template <uint32_t NW, uint32_t ENC>
 struct XDma {
     static constexpr uint32_t PER_WAVE = (XD_INSTRS + NW - 1) / NW;
     uint32_t off[PER_WAVE];
@@ -518,10 +532,10 @@ struct XDma {
         for (uint32_t t = 0; t < PER_WAVE; ++t) {
             const uint32_t slot = 64 * min(first + t * NW, XD_INSTRS - 1) + lane;
             const uint32_t row = min(slot / 9, last_row), chunk = slot % 9;
-            off[t] = (uint32_t)(((uint64_t)row * in_stride + 8 * (chunk == 8 ? 0 : chunk)) * 2);
+            off[t] = (uint32_t)(((uint64_t)row * in_stride + slab_chunk_col<ENC>(chunk == 8 ? 0 : chunk)) * 2);
         }
     }
-    // copies columns k0..k0+63 of the tile's rows into lds_tile
+    // copies slab columns (k0 + slab_chunk_col) of the tile's rows into lds_tile
     __device__ __forceinline__ void copy(const _Float16 *__restrict__ x, uint64_t in_stride, uint32_t m_base,
                                          uint32_t k0, _Float16 *lds_tile) const {
         const char *base = (const char *)(x + (uint64_t)m_base * in_stride + k0);
@@ -619,13 +633,13 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
     XLoad<XT> xr[SP];
     WRaw<ENC> wA[SP], wB[SP];
     const uint32_t ksteps = columns / BK;
-    XDma<NW> xd;
+    XDma<NW, ENC> xd;
     if constexpr (DMA) {
         xd.init(in_stride, m_base, tokens, wave, lane);
         xd.copy((const _Float16 *)x, in_stride, m_base, 0, pf_smem);
     } else {
 #pragma unroll
-        for (uint32_t s_ = 0; s_ < SP; ++s_) xr[s_].load(xrow + NUQ_PF_PART(s_) * 32, xvalid);
+        for (uint32_t s_ = 0; s_ < SP; ++s_) xr[s_].load(xrow + slab_chunk_col<ENC>(4 * NUQ_PF_PART(s_)), xvalid);
     }
 #pragma unroll
     for (uint32_t s_ = 0; s_ < SP; ++s_) wA[s_].load(wrow, 0, NUQ_PF_PART(s_));
@@ -663,10 +677,10 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
         }                                                                                                          \
         if (next) {                                                                                                \
             if constexpr (DMA) {                                                                                   \
-                xd.copy((const _Float16 *)x, in_stride, m_base, (ks_ + 1) * BK, pf_smem + (cur ^ 1) * XS);        \
+                xd.copy((const _Float16 *)x, in_stride, m_base, slab_k0<ENC>(ks_ + 1), pf_smem + (cur ^ 1) * XS);  \
             } else {                                                                                               \
                 _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_)                                             \
-                    xr[s_].load(xrow + NUQ_PF_PART(s_) * 32 + (ks_ + 1) * BK, xvalid);                             \
+                    xr[s_].load(xrow + slab_chunk_col<ENC>(4 * NUQ_PF_PART(s_)) + slab_k0<ENC>(ks_ + 1), xvalid);  \
             }                                                                                                      \
         }                                                                                                          \
         if (PF_COPY_FIRST<ENC>::value && far_) {                                                                   \
