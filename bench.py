@@ -56,6 +56,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default="", help="comma list of: configs, prefill (the headline GEMV always runs)")
+    p.add_argument("--case", default="",
+                   help="profiling aid: only time one matmul, ENC:ROWS:COLUMNS:TOKENS (f16 activations), e.g. 14:5120:17408:4096")
     p.add_argument("--profile-copy", action="store_true",
                    help="also run one plain 256 MiB device copy (the calibration kernel for rocprofv3 byte counters)")
     return p.parse_args()
@@ -400,6 +402,13 @@ def main():
 
     def want(name):
         return not only or name in only
+
+    if args.case:
+        e, r, c, t = (int(v) for v in args.case.split(":"))
+        d = bench_gemm(torch, nq, backend, stream, e, r, c, t, reps=10, warmup=2)
+        print(json.dumps({"case": args.case, "ms": d["ms"], "tflops": d["tflops"]}))
+        backend.close()
+        return
 
     # headline: configs[1] gate/up GEMV, exactly --steps launches timed
     enc, rows, columns, seed = CONFIGS["c2_gate"]
