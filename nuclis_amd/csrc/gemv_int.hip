@@ -749,7 +749,11 @@ __device__ __forceinline__ float group_sum(float v) {
 template <uint32_t ENC>
 constexpr int gd_threads() { return ENC == 14 ? 768 : GI_WG_THREADS; }
 
-template <uint32_t ENC, int SLOTS, int D>
+// TWO: x takes two rounds of half-slices (a template parameter, so each
+// form is straight-line code: the asm loads' registers must not be touched
+// before their explicit waits, and a branch merging two forms made the
+// compiler copy them early).
+template <uint32_t ENC, int SLOTS, int D, bool TWO = false>
 __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
@@ -851,14 +855,30 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     const uint32_t t0 = threadIdx.x;
     XHalf xh;
     if (t0 < 2 * nslices) load_half_slice_asm(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
+    // When x takes a second round of half-slices (long rows: 1088 for
+    // K = 17408 over 576 threads), its loads go out with the first, before
+    // the copies, instead of after the first round's quantisation. The
+    // condition is uniform, and every thread issues the loads (clamped to
+    // the last half-slice) so the wait counts below are exact.
+    constexpr bool two_rounds = TWO;
+    XHalf xh2;
+    const uint32_t t1 = min(t0 + blockDim.x, 2 * nslices - 1);
+    if constexpr (two_rounds) load_half_slice_asm(x + (uint64_t)(t1 >> 1) * 32, t1 & 1, xh2);
 #pragma unroll
     for (int d = 0; d < D; ++d) NUQ_GD_DMA(d, (uint32_t)d)
 
     // The slice image goes to LDS through asm and the barrier carries no
     // fence, so the copies in flight keep flying while x is quantised.
-    xhalf_wait<GD_DMA_INSTRS * D>(xh);  // x is older than the D steps' copies
-    if (t0 < 2 * nslices) quantize_half_slice<true>(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
-    for (uint32_t t = t0 + blockDim.x; t < 2 * nslices; t += blockDim.x) {
+    if constexpr (two_rounds) {
+        xhalf_wait<GD_DMA_INSTRS * D + 4>(xh);  // x is older than the second round and the copies
+        if (t0 < 2 * nslices) quantize_half_slice<true>(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
+        xhalf_wait<GD_DMA_INSTRS * D>(xh2);
+        if (t0 + blockDim.x < 2 * nslices) quantize_half_slice<true>(xh2, t1 & 1, slices + (t1 >> 1) * SLICE_WORDS);
+    } else {
+        xhalf_wait<GD_DMA_INSTRS * D>(xh);  // x is older than the D steps' copies
+        if (t0 < 2 * nslices) quantize_half_slice<true>(xh, t0 & 1, slices + (t0 >> 1) * SLICE_WORDS);
+    }
+    for (uint32_t t = t0 + 2 * blockDim.x; t < 2 * nslices; t += blockDim.x) {
         load_half_slice_asm(x + (uint64_t)(t >> 1) * 32, t & 1, xh);
         xhalf_wait<0>(xh);
         quantize_half_slice<true>(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
@@ -962,9 +982,13 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     const size_t lds = lds_for(sets);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
-    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)),
-                       dim3(64 * waves), lds, s, w, stride, rows, nblocks, rows_per_wg, set_waves, x, y,
-                       tail ? 1u : 0u, GdSegments{});
+    const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)), block(64 * waves);
+    if (2 * nblocks * 8 > 64 * waves)  // x in two rounds of half-slices (or more)
+        hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, true>), grid, block, lds, s, w, stride, rows, nblocks,
+                           rows_per_wg, set_waves, x, y, tail ? 1u : 0u, GdSegments{});
+    else
+        hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, false>), grid, block, lds, s, w, stride, rows, nblocks,
+                           rows_per_wg, set_waves, x, y, tail ? 1u : 0u, GdSegments{});
     return hipGetLastError();
 }
 
@@ -1010,8 +1034,12 @@ static hipError_t launch_dma_segments(hipStream_t s, uint32_t count, const uint8
     while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
     const size_t lds = lds_for(sets);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D>), dim3(wgs), dim3(64 * set_waves * sets), lds, s, w[0], stride,
-                       rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
+    if (2 * nblocks * 8 > 64 * set_waves * sets)
+        hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, true>), dim3(wgs), dim3(64 * set_waves * sets), lds, s,
+                           w[0], stride, rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
+    else
+        hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, false>), dim3(wgs), dim3(64 * set_waves * sets), lds, s,
+                           w[0], stride, rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
     return hipGetLastError();
 }
 

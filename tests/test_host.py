@@ -145,3 +145,23 @@ def test_gguf_reader_survives_corruption_under_sanitizers():
     subprocess.run(["make", "-s", "-C", str(d), "fuzz"], check=True, capture_output=True, timeout=300)
     r = subprocess.run([str(d / "_build" / "gguf_fuzz")], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and "gguf_fuzz: OK" in r.stdout, r.stdout + r.stderr
+
+
+def test_gemv_asm_loads_are_not_read_before_their_waits():
+    """The decode GEMV's activation loads are inline asm waited for by a
+    later inline-asm s_waitcnt; the compiled gfx950 code must not read (or
+    copy) their destination registers in between (tests/isa/asm_hazard.py)."""
+    import subprocess
+    import tempfile
+    from tests.isa.asm_hazard import hazards
+    root = Path(__file__).resolve().parents[1]
+    with tempfile.TemporaryDirectory() as d:
+        out = Path(d) / "gemv_int.s"
+        subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17",
+                        "-I", str(root / "include"), "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                        "-fno-gpu-flush-denormals-to-zero", "--cuda-device-only", "-S",
+                        str(root / "nuclis_amd" / "csrc" / "gemv_int.hip"), "-o", str(out)],
+                       check=True, capture_output=True)
+        count, found = hazards(out.read_text())
+    assert count >= 10, count
+    assert not found, found[:5]
