@@ -81,3 +81,43 @@ def test_noalloc_segments_match_the_allocating_entry_point():
     finally:
         L.nuq_destroy(ctx)
         ref.close()
+
+
+def test_noalloc_segments_under_graph_capture():
+    """The allocation-free entry point captured in a HIP graph on a fresh
+    context (no workspace, none allocated): every replay, with eager work
+    and synchronizations between replays, equals the eager result."""
+    import torch
+    L = nq.lib()
+    err = ctypes.create_string_buffer(256)
+    ctx = L.nuq_create(0, err, len(err))
+    try:
+        rows, columns = 8192, 5120
+        x = to_gpu(gaussian(85, columns))
+        gate = nq.Matrix(12, rows, columns, to_gpu(nq.quantize(12, gaussian(86, (rows, columns), 0.02))))
+        up = nq.Matrix(12, rows, columns, to_gpu(nq.quantize(12, gaussian(87, (rows, columns), 0.02))))
+        eager = torch.full((rows,), np.nan, device="cuda")
+        assert call(L.nuq_matvec_segments_noalloc, ctx, [(gate, eager), (up, eager)], x,
+                    nq.SEGMENT_SILU_MUL_PAIR) == 0
+        out = torch.full((rows,), np.nan, device="cuda")
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        arr = segs([(gate, out), (up, out)])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            assert L.nuq_set_stream(ctx, stream.cuda_stream) == 0
+            with torch.cuda.graph(graph, stream=stream):
+                assert L.nuq_matvec_segments_noalloc(ctx, arr, 2, x.data_ptr(), nq.SEGMENT_SILU_MUL_PAIR) == 0
+        for _ in range(4):
+            out.fill_(np.nan)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            scratch_user = torch.full((rows,), 3.0, device="cuda")  # eager work between replays
+            assert call(L.nuq_matvec_segments_noalloc, ctx, [(gate, scratch_user), (up, scratch_user)], x,
+                        nq.SEGMENT_SILU_MUL_PAIR) == 0
+            assert torch.equal(scratch_user, eager)
+        assert L.nuq_workspace_bytes(ctx) == 0
+    finally:
+        L.nuq_destroy(ctx)
