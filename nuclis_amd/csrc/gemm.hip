@@ -1385,6 +1385,11 @@ __global__ void __launch_bounds__(64 * VF_MAX_WAVES) verify_split_kernel(const u
 // SIMD), runs of 3 need 256 (2 per SIMD)
 template <uint32_t NB>
 constexpr uint32_t vd_max_waves() { return NB == 2 ? 12 : 8; }
+// Blocks per K range of the streamed verify tile. The F32 multi-token form
+// (xs3) stages three f16 part rows per token in each wave's region: at 20
+// blocks its 10 waves take 10 x 13.8 KB with three ring slots, and a CU's
+// rows' partial sums still fit beside them (K = 5120 runs as one range).
+constexpr uint32_t vd_max_kb(bool xs3) { return xs3 ? 20 : 2 * vd_max_waves<2>(); }
 
 typedef __attribute__((address_space(3))) uint8_t vd_lds_u8_t;
 __device__ __forceinline__ uint32_t vd_lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(const vd_lds_u8_t *)p; }
@@ -1630,7 +1635,6 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
             // rows pT + t), the F32 sums of 32-value groups go to the lanes
             // that need them, and the wave agrees on the token's scale 2^e
             static_assert(STAGE == 1, "F32 activations are staged in the wave's own region");
-            NUQ_VD_DMA(0, 0)
             (void)xchunks;
             (void)span_log2;
             // (LDS accesses as asm: see vd_read_x)
@@ -1757,34 +1761,43 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         for (uint32_t d = 1; d < DEPTH; ++d)
             if (d < nsteps) NUQ_VD_DMA(d, d)
     } else {
-#pragma unroll
-        for (uint32_t d = 0; d < DEPTH; ++d)
-            if (d < nsteps) NUQ_VD_DMA(d, d)
-
-        // x fragments of the wave's blocks, loaded after the first copies are
-        // on their way. A rows past `tokens` are zero; they reach only D rows
-        // that are never stored.
+        // x fragments of the wave's blocks, loaded directly and before the
+        // first copies, so that they are waited for alone (loads return in
+        // order). Every lane loads (lanes of tokens past `tokens` read token
+        // 0) and those A rows are zeroed afterwards: they reach only D rows
+        // that are never stored. The loads are unconditional so that they all
+        // go out before the first wait.
         const bool tok_ok = r16 < tokens;
         const XT *xrow = x + (uint64_t)(tok_ok ? r16 : 0) * in_stride;
+        using XV = typename std::conditional<sizeof(XT) == 2, half8, float4>::type;
+        constexpr int XP = sizeof(XT) == 2 ? 1 : 2;  // 16-byte loads per chunk
+        XV xv[NB][8][XP];
 #pragma unroll
         for (uint32_t s = 0; s < NB; ++s) {
             const uint32_t blk = s < nlive ? b0 + s : b0;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 const uint32_t col = blk * L::BLOCK_VALUES + L::col(h, c);
-                bx[s][c] = half8{};
-                if (tok_ok) {
-                    if constexpr (sizeof(XT) == 2) {
-                        bx[s][c] = *(const half8 *)((const _Float16 *)xrow + col);
-                    } else {
-                        const float4 f0 = *(const float4 *)((const float *)xrow + col);
-                        const float4 f1 = *(const float4 *)((const float *)xrow + col + 4);
-                        bx[s][c] = half8{(_Float16)f0.x, (_Float16)f0.y, (_Float16)f0.z, (_Float16)f0.w,
-                                         (_Float16)f1.x, (_Float16)f1.y, (_Float16)f1.z, (_Float16)f1.w};
-                    }
-                }
+#pragma unroll
+                for (int p = 0; p < XP; ++p) xv[s][c][p] = *(const XV *)(xrow + col + 8 / XP * p);
             }
         }
+#pragma unroll
+        for (uint32_t d = 0; d < DEPTH; ++d)
+            if (d < nsteps) NUQ_VD_DMA(d, d)
+#pragma unroll
+        for (uint32_t s = 0; s < NB; ++s)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                if constexpr (sizeof(XT) == 2) {
+                    bx[s][c] = xv[s][c][0];
+                } else {
+                    const float4 f0 = xv[s][c][0], f1 = xv[s][c][1];
+                    bx[s][c] = half8{(_Float16)f0.x, (_Float16)f0.y, (_Float16)f0.z, (_Float16)f0.w,
+                                     (_Float16)f1.x, (_Float16)f1.y, (_Float16)f1.z, (_Float16)f1.w};
+                }
+                if (!tok_ok) bx[s][c] = half8{};
+            }
     }
 
 #pragma unroll
@@ -1939,9 +1952,7 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // K ranges: longer rows (the down projection) run as `ranges` ranges of
     // kb blocks over the workgroups, into the prefill workspace
     uint32_t ranges = 1, kb = nblocks_all;
-    // (xs3: at most 18 blocks per range, so 9 waves' regions hold the
-    // three part rows per token beside the step-0 slot)
-    const uint32_t max_kb = xs3 ? 18 : 2 * MAXW;
+    const uint32_t max_kb = vd_max_kb(xs3);
     if (nblocks_all > max_kb) {
         ranges = (nblocks_all + max_kb - 1) / max_kb;
         kb = (nblocks_all + ranges - 1) / ranges;
@@ -2118,10 +2129,10 @@ uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t column
                                uint64_t in_stride, bool xs3) {
     if (tokens <= 16 && columns % 256 == 0) {
         // the streamed verify tile's K ranges (Q4_K / Q5_K rows longer than
-        // 2 * MAXW blocks, or 18 for the F32 multi-token form), one F32
+        // 2 * MAXW blocks, or 20 for the F32 multi-token form), one F32
         // partial per range, token and row
         constexpr uint32_t MAXW = vd_max_waves<2>();
-        const uint32_t nblocks = columns / 256, max_kb = xs3 ? 18 : 2 * MAXW;
+        const uint32_t nblocks = columns / 256, max_kb = vd_max_kb(xs3);
         if ((encoding != 12 && encoding != 13) || nblocks <= max_kb || rows < 16) return 0;
         return (uint64_t)((nblocks + max_kb - 1) / max_kb) * tokens * rows;
     }

@@ -864,6 +864,9 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     XHalf xh2;
     const uint32_t t1 = min(t0 + blockDim.x, 2 * nslices - 1);
     if constexpr (two_rounds) load_half_slice_asm(x + (uint64_t)(t1 >> 1) * 32, t1 & 1, xh2);
+    // With two rounds, every wave's x loads go out before any wave's copies
+    // (5120 x 17408: 16.2 -> 15.6 us for Q4_K, 19.5 -> 18.8 us for Q5_K).
+    if constexpr (two_rounds) __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int d = 0; d < D; ++d) NUQ_GD_DMA(d, (uint32_t)d)
 

@@ -612,8 +612,9 @@ def test_matvec_nan_activation_poisons_rows(backend, encoding):
 # parts holding every bit of x, so the plain F32 bound applies.
 # (From four tokens the f16 tile takes over, as the reference's half tiles
 # do from four tokens, ops/matmul.zig:86-108.)
-MULTI_TOKEN_CASES = [(e, r, c, t) for (e, r, c) in [(12, 17408, 5120), (12, 5120, 17408), (13, 1040, 5120),
-                                                    (12, 40, 1280), (12, 1000, 4608), (13, 520, 17408)]
+MULTI_TOKEN_CASES = [(e, r, c, t) for (e, r, c) in [(12, 17408, 5120), (12, 5120, 17408), (13, 17408, 5120),
+                                                    (13, 1040, 5120), (12, 40, 1280), (12, 1000, 4608),
+                                                    (13, 520, 17408)]
                      for t in (2, 3)]
 
 
