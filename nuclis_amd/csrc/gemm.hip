@@ -1610,14 +1610,25 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     // fixed 32-bit offset, so a copy costs no VALU. Every offset stays in
     // the workgroup's rows, so the record count is left at its maximum.
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(vd_lds_addr(ring));
+    // DEPTH 1 (VS): one register set per wave instead of ring slots: step
+    // i + 1's 16-byte pieces are loaded into registers while step i computes
+    // and written to the wave's single slot at the top of step i + 1.
+    constexpr bool VS = DEPTH == 1;
+    u32x4 vr[V::INSTRS];
 #define NUQ_VD_DMA(SLOT_, STEP_)                                                                          \
     {                                                                                                   \
+    if constexpr (VS) {                                                                                 \
+        const uint32_t soff_ = min(16 * (STEP_), nrow - 16) * (uint32_t)stride;                         \
+        _Pragma("unroll") for (uint32_t n = 0; n < V::INSTRS; ++n) vr[n] =                              \
+            __builtin_nontemporal_load((const u32x4 *)(wg_base + soff_ + doff[n]));                     \
+    } else {                                                                                            \
         const uint32_t soff_ = min(16 * (STEP_), nrow - 16) * (uint32_t)stride;                         \
         const uint32_t dst_ = ring_lds + (SLOT_) * slot_stride;                                         \
         _Pragma("unroll") for (uint32_t n = 0; n < V::INSTRS; ++n) {                                    \
             if (64 * (n + 1) <= V::STEP_CHUNKS || 64 * n + lane < V::STEP_CHUNKS)                          \
                 vd_copy(wg_base, dst_ + n * 1024, doff[n], soff_);                                      \
         }                                                                                               \
+    }                                                                                                   \
     }
     half8 bx[NB][8];
     float sx3[NB][2], sft[4];  // XS = 3: F32 group sums; each token's scale back
@@ -1839,14 +1850,26 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     for (uint32_t i = 0; i < nsteps; ++i) {
         uint4 hd[NB][L::NH], cq[NB][2];
         const uint32_t a = ring_a + slot * slot_stride;
-        // the copies of up to DEPTH - 1 younger steps may still be in flight
-        const uint32_t ahead = min(DEPTH - 1, nsteps - 1 - i);
-        if (DEPTH > 2 && ahead >= 2)
-            vd_ring_read<ENC, NB, 2 * V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
-        else if (ahead >= 1)
-            vd_ring_read<ENC, NB, V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
-        else
-            vd_ring_read<ENC, NB, 0>(a, a + L::CODE + 32 * h, hd, cq);
+        if constexpr (VS) {
+            // the step's pieces go to the slot (the compiler waits for their
+            // loads), the next step's loads go out, and the slot is read back
+            // (LDS operations of a wave complete in order)
+#pragma unroll
+            for (uint32_t n = 0; n < V::INSTRS; ++n)
+                if (64 * (n + 1) <= V::STEP_CHUNKS || 64 * n + lane < V::STEP_CHUNKS)
+                    *(u32x4 *)(ring + n * 1024 + 16 * lane) = vr[n];
+            if (i + 1 < nsteps) NUQ_VD_DMA(0, i + 1)
+            vd_ring_read<ENC, NB, 63>(a, a + L::CODE + 32 * h, hd, cq);
+        } else {
+            // the copies of up to DEPTH - 1 younger steps may still be in flight
+            const uint32_t ahead = min(DEPTH - 1, nsteps - 1 - i);
+            if (DEPTH > 2 && ahead >= 2)
+                vd_ring_read<ENC, NB, 2 * V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
+            else if (ahead >= 1)
+                vd_ring_read<ENC, NB, V::INSTRS>(a, a + L::CODE + 32 * h, hd, cq);
+            else
+                vd_ring_read<ENC, NB, 0>(a, a + L::CODE + 32 * h, hd, cq);
+        }
         // one copy of the step body per live block count (wave-uniform), so
         // the per-block results need no merging
         static_assert(NB == 2, "live block counts 1 and 2");
@@ -1869,8 +1892,10 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         // the slot's refill goes out after the step's arithmetic: a copy that
         // waits for room in the memory queue then holds up no arithmetic
         // (17408 x 5120: M=8 17.9 -> 17.5 us, T=2 18.3 -> 17.5 us)
-        if (i + DEPTH < nsteps) NUQ_VD_DMA(slot, i + DEPTH)
-        slot = slot + 1 == DEPTH ? 0 : slot + 1;
+        if constexpr (!VS) {
+            if (i + DEPTH < nsteps) NUQ_VD_DMA(slot, i + DEPTH)
+            slot = slot + 1 == DEPTH ? 0 : slot + 1;
+        }
     }
 #undef NUQ_VD_DMA
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
@@ -1908,8 +1933,10 @@ static hipError_t launch_verify_dma_nb(hipStream_t s, const uint8_t *w, uint64_t
 #define NUQ_VD_LAUNCH_D(XT_, MODE_, XS_)                                                                     \
     if (L.depth == 3)                                                                                       \
         NUQ_VD_LAUNCH(XT_, MODE_, 3, XS_);                                                                  \
+    else if (L.depth == 2)                                                                                  \
+        NUQ_VD_LAUNCH(XT_, MODE_, 2, XS_);                                                                  \
     else                                                                                                    \
-        NUQ_VD_LAUNCH(XT_, MODE_, 2, XS_);
+        NUQ_VD_LAUNCH(XT_, MODE_, 1, XS_);
     if (xs3) {
         NUQ_VD_LAUNCH_D(float, 1, 3)
     } else if (x_f16 && L.stage == 1) {
@@ -1988,7 +2015,8 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // at most one row.
     const uint32_t want_rows = std::max(16u, (rows * ranges + 255) / 256);
     // Candidates in order of preference: three ring slots (two steps in
-    // flight while one computes), then two; within each, private staging,
+    // flight while one computes), then two (Q4_K without xs3: the single
+    // register-staged slot); within each, private staging,
     // shared staging, direct loads (the only one for F32 activations). The
     // first whose rings and partial sums hold want_rows rows wins, else the
     // one holding the most.
@@ -1997,7 +2025,12 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     const int modes_f16[3] = {1, 2, 0}, modes_f32[1] = {0}, modes_xs3[1] = {1};
     const int *modes = xs3 ? modes_xs3 : x_f16 ? modes_f16 : modes_f32;
     bool found = false;
-    for (uint32_t depth = 3; depth >= 2 && !found; --depth) {
+    // Q4_K with one token row per MFMA row (not xs3) stages each step through
+    // registers (depth 1): 17408 x 5120 at M=8 took 16.3-16.7 us against
+    // 17.7 with the three-slot ring. The register set spills on Q5_K and
+    // with xs3, which keep the rings.
+    const bool vs = ENC == 12 && !xs3;
+    for (uint32_t depth = vs ? 1 : 3; depth >= (vs ? 1u : 2u) && !found; --depth) {
         for (int m = 0; m < (x_f16 ? 3 : 1); ++m) {
             const int mode = modes[m];
             VdLayout c{};
