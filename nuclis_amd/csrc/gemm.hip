@@ -1639,7 +1639,9 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         static_assert(NB <= 2, "a run's activations are 32 or 64 chunks per token");
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
         const uint32_t span_log2 = nlive == 2 ? 6 : 5;  // log2(span / 16)
-        uint8_t *xs = STAGE == 1 ? ring + V::SLOT : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
+        // (VS: in the slot itself, whose first step waits in registers until
+        // the activations are read)
+        uint8_t *xs = STAGE == 1 ? (VS ? ring : ring + V::SLOT) : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
         if constexpr (XS == 3) {
             // F32 activations: lane k converts values [8k, 8k + 8) of the
             // wave's run of each token into its three f16 parts (staging
@@ -2038,7 +2040,8 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
             c.depth = depth;
             c.per_row = per_row;
             const size_t ahead = (depth - 1) * slot;  // staging room from slot 1 on
-            c.region = (uint32_t)(mode == 1 ? depth * slot + (xwave > ahead ? xwave - ahead : 0)
+            c.region = (uint32_t)(mode == 1 ? (depth == 1 ? std::max(slot, xwave)
+                                                          : depth * slot + (xwave > ahead ? xwave - ahead : 0))
                                             : mode == 2 ? slot : depth * slot);
             c.slot_gap = (uint32_t)(mode == 2 ? waves * slot : slot);
             const size_t rings = mode == 2 ? depth * waves * slot : (size_t)waves * c.region;
