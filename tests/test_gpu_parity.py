@@ -639,3 +639,44 @@ def test_multi_token_f32_matches_oracle(backend, encoding, rows, columns, tokens
     got = out.cpu().numpy()[:, :rows]
     check_close(got, want, mass(encoding, w, rows, columns, x), F32_K, f"multitoken {encoding}")
     assert np.array_equal(got.view(np.uint32), out2.cpu().numpy()[:, :rows].view(np.uint32))
+
+
+# Graph replays of the streamed kernels: the matmul routes (decode GEMV,
+# F32 multi-token, verify tile with register-staged or ringed steps, K ranges
+# with their reduce, prefill) captured in a HIP graph, replayed with eager
+# work between replays, must equal the eager result bit for bit. Copies or
+# loads read before they land would show up here as replay differences.
+GRAPH_CASES = [(12, 2048, 5120, 1, "f32"), (12, 4104, 5120, 8, "f16"), (12, 4104, 5120, 8, "f32"),
+               (12, 17408, 5120, 2, "f32"), (13, 4104, 5120, 3, "f32"), (13, 4104, 5120, 8, "f16"),
+               (12, 1040, 17408, 8, "f16"), (12, 1024, 5120, 512, "f16")]
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens,xdtype", GRAPH_CASES)
+def test_matmul_graph_replays_match_eager(backend, encoding, rows, columns, tokens, xdtype):
+    import torch
+    w = quantized(encoding, rows, columns, 110 + tokens)
+    x = gaussian(111 + tokens, (tokens, columns))
+    xg = to_gpu(x.astype(np.float16)) if xdtype == "f16" else to_gpu(x)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    print(f"[graph] enc {encoding} {rows}x{columns} tokens {tokens} {xdtype}", flush=True)
+    eager = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matmul(m, xg, columns, eager, rows, tokens)  # also sizes the lazy workspace
+    backend.sync()
+    out = torch.full((tokens, rows), np.nan, device="cuda")
+    other = torch.empty((tokens, rows), device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            backend.matmul(m, xg, columns, out, rows, tokens)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(np.nan)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
+        backend.matmul(m, xg, columns, other, rows, tokens)  # eager work between replays
+        backend.sync()
+        assert torch.equal(other.view(torch.int32), eager.view(torch.int32))
