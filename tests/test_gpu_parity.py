@@ -680,3 +680,30 @@ def test_matmul_graph_replays_match_eager(backend, encoding, rows, columns, toke
         backend.matmul(m, xg, columns, other, rows, tokens)  # eager work between replays
         backend.sync()
         assert torch.equal(other.view(torch.int32), eager.view(torch.int32))
+
+
+# matvecRows with 4..8 F32 token rows (Q4_K / Q5_K) runs as launches of the
+# F32 multi-token MFMA form over 3 and 2 tokens: within the plain F32 bound,
+# and each chunk's tokens bit-identical to the same tokens served alone.
+@pytest.mark.parametrize("encoding,rows,columns", [(12, 4104, 5120), (13, 1040, 5120), (12, 1040, 17408)])
+@pytest.mark.parametrize("tokens", [4, 5, 8])
+def test_matvec_rows_in_chunks_matches_oracle(backend, encoding, rows, columns, tokens):
+    import torch
+    w = quantized(encoding, rows, columns, 120 + tokens)
+    x = gaussian(121 + tokens, (tokens, columns))
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    xg = to_gpu(x)
+    print(f"[rows-chunks] enc {encoding} {rows}x{columns} T={tokens}", flush=True)
+    out = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matvec_rows(m, xg, columns, out, rows, tokens)
+    out2 = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, out2, rows, tokens)
+    first = 2 if tokens == 4 else 3
+    alone = torch.full((first, rows), np.nan, device="cuda")
+    backend.matvec_rows(m, xg[:first].contiguous(), columns, alone, rows, first)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, x)
+    got = out.cpu().numpy()
+    check_close(got, want, mass(encoding, w, rows, columns, x), F32_K, f"rows-chunks {encoding}")
+    assert np.array_equal(got.view(np.uint32), out2.cpu().numpy().view(np.uint32))
+    assert np.array_equal(got[:first].view(np.uint32), alone.cpu().numpy().view(np.uint32))
