@@ -1,0 +1,59 @@
+"""Seeded random shapes through the routed matmul entry (every encoding,
+token counts across the GEMV, multi-token, verify-tile and prefill routes,
+f16 and F32 activations) against the CPU oracle. Each case prints its shape
+before it runs."""
+import numpy as np
+import pytest
+
+import nuclis_amd as nq
+from nuclis_amd.synth import gaussian
+from oracle import oracle as orc
+from tests.gpu_util import F16_K, F32_K, check_close, mass, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+ENCODINGS = [8, 12, 13, 14, 23]
+TOKENS = [1, 2, 3, 4, 5, 8, 9, 16, 17, 100, 129, 300]
+
+
+def cases(n=30, n_prefill=8, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n + n_prefill:
+        enc = int(rng.choice(ENCODINGS))
+        # the last n_prefill cases take the prefill route (over 128 tokens)
+        tokens = int(rng.choice(TOKENS)) if len(out) < n else int(rng.integers(129, 600))
+        rows = int(rng.integers(1, 750)) * 8
+        columns = int(rng.integers(1, 49)) * 256
+        if rows * columns * tokens > 1.5e9:
+            continue
+        xdtype = "f32" if tokens == 1 else str(rng.choice(["f16", "f32"]))
+        out.append((enc, rows, columns, tokens, xdtype, int(rng.integers(1 << 20))))
+    return out
+
+
+@pytest.fixture(scope="module")
+def backend():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    b = nq.Backend(0)
+    yield b
+    b.close()
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens,xdtype,seed", cases())
+def test_random_shape_matmul_matches_oracle(backend, encoding, rows, columns, tokens, xdtype, seed):
+    import torch
+    print(f"[random] enc {encoding} {rows}x{columns} tokens {tokens} {xdtype} seed {seed}", flush=True)
+    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+    x32 = gaussian(seed + 1, (tokens, columns))
+    xref = x32.astype(np.float16).astype(np.float32) if xdtype == "f16" else x32
+    xg = to_gpu(x32.astype(np.float16)) if xdtype == "f16" else to_gpu(x32)
+    out = torch.full((tokens, rows), np.nan, dtype=torch.float32, device="cuda")
+    backend.matmul(nq.Matrix(encoding, rows, columns, to_gpu(w)), xg, columns, out, rows, tokens)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, xref)
+    # F32 precision: the decode GEMV and the 2-3 token rows; the tiles round
+    # activations (and some weights) to f16
+    k = F32_K if xdtype == "f32" and tokens <= 3 else F16_K
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, f"random {encoding}")
