@@ -2075,6 +2075,8 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     wgs = std::min(wgs, rows / 16);
     const uint32_t rows_per_wg = (rows + wgs - 1) / wgs;  // the longest range
     if (rows_per_wg > best_rows) return false;
+    // a range's copy offsets (step base + lane offset) are 32-bit
+    if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return false;
     const size_t xall_lds = L.stage == 2 ? waves * slot + xall : 0;
     L.lds = std::max(rings_end + rows_per_wg * L.per_row, xall_lds);
     *err = launch_verify_dma_nb<ENC, 2>(s, w, stride, rows, nblocks_all, x, x_f16, in_stride, y, out_stride, tokens,
