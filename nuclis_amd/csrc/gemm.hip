@@ -1585,8 +1585,12 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     const uint32_t nrow = (uint32_t)((uint64_t)(blockIdx.x + 1) * rows / gridDim.x) - row_begin;
     const uint32_t nsteps = (nrow + 15) / 16;
     // wave kw owns blocks [kw nblocks / nwaves, (kw + 1) nblocks / nwaves)
-    const uint32_t b0 = __builtin_amdgcn_readfirstlane(kw * nblocks / nwaves);
-    const uint32_t nlive = __builtin_amdgcn_readfirstlane((kw + 1) * nblocks / nwaves - b0);  // 1 .. NB
+    // NB = 3: runs of 3 blocks on the first nblocks - 2 nwaves waves, 2 on the
+    // rest, so with 8 waves each SIMD's two waves (kw, kw + 4) hold 5 blocks
+    const uint32_t x3 = NB == 3 ? nblocks - 2 * nwaves : 0;
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane(NB == 3 ? 2 * kw + min(kw, x3) : kw * nblocks / nwaves);
+    const uint32_t nlive = __builtin_amdgcn_readfirstlane(NB == 3 ? 2 + (kw < x3 ? 1 : 0)
+                                                                   : (kw + 1) * nblocks / nwaves - b0);  // 1 .. NB
 
     // This lane's chunk of each copy: row q of the step and byte offset in
     // the row (chunks past the step repeat the last one; a block past the
@@ -1636,7 +1640,7 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     if constexpr (STAGE != 0) {
         // this wave's activations, [token][its blocks' 512 bytes], copied
         // before the step-0 weights so that they are waited for alone
-        static_assert(NB <= 2, "a run's activations are 32 or 64 chunks per token");
+        static_assert(NB <= 2 || (XS == 1 && STAGE == 1), "a run's activations are 32, 64 or 96 chunks per token");
         const uint32_t span = nlive * 512, xchunks = tokens * span / 16;
         const uint32_t span_log2 = nlive == 2 ? 6 : 5;  // log2(span / 16)
         // (VS: in the slot itself, whose first step waits in registers until
@@ -1725,7 +1729,8 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
             for (uint32_t jx = 0; 64 * jx < xchunks; ++jx) {
                 const uint32_t k = 64 * jx + lane;
                 if (k < xchunks) {
-                    const uint32_t t = k >> span_log2, rem = k & ((1u << span_log2) - 1);
+                    const uint32_t t = nlive == 3 ? k / 96 : k >> span_log2;
+                    const uint32_t rem = k - t * (span / 16);
                     const uint8_t *src = (const uint8_t *)x + ((uint64_t)t * in_stride + b0 * L::BLOCK_VALUES) * 2 + rem * 16;
                     __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)(xs + 1024 * jx), 16, 0, 0);
                 }
@@ -1874,9 +1879,9 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         }
         // one copy of the step body per live block count (wave-uniform), so
         // the per-block results need no merging
-        static_assert(NB == 2, "live block counts 1 and 2");
+        static_assert(NB == 2 || NB == 3, "live block counts 1 and 2, or 2 and 3");
         const floatx4 acc = nlive == NB ? vd_step_blocks<L, NB, NB, XS>(hd, cq, h, bx, sx, sfm)
-                                        : vd_step_blocks<L, NB, 1, XS>(hd, cq, h, bx, sx, sfm);
+                                        : vd_step_blocks<L, NB, NB - 1, XS>(hd, cq, h, bx, sx, sfm);
         // D: lane holds row base + r16 (base = min(16 i, nrow - 16)), tokens
         // 4h..4h+3; rows an earlier step stored are skipped (written through
         // asm: the compiler would otherwise wait for every ring copy in flight)
@@ -2000,6 +2005,45 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     // At K = 20 blocks this measured faster than 8 waves of 3 + 2 blocks per
     // SIMD (one wave left alone on its SIMD at the end) and than 12 waves of
     // 1 or 2 blocks (5 blocks on every SIMD, but more per-wave overhead).
+    // Q4_K rows split into K ranges of 17-24 blocks (the down projection's
+    // 68 blocks: 23 + 23 + 22) with f16 activations run on 8 waves of 3- and
+    // 2-block runs (NB = 3, register-staged): 5120 x 17408 at M=8 went from
+    // 19.6 to 18.4-18.6 us. At K = 5120 (one range of 20 blocks) it measured
+    // no better than 10 waves of 2 blocks, which keep that shape.
+    if constexpr (ENC == 12) {
+        const uint32_t last = nblocks_all - (ranges - 1) * kb;  // the last range's blocks
+        if (!xs3 && x_f16 && ranges > 1 && kb >= 17 && kb <= 24 && last >= 17) {
+            constexpr uint32_t W3 = 8;
+            const uint32_t tpad3 = (tokens + 3) & ~3u;
+            const size_t slot3 = VDma<ENC, 3>::SLOT;
+            const size_t region3 = std::max(slot3, (size_t)tokens * 3 * 512);
+            const size_t rings3 = W3 * region3;
+            const size_t per_row3 = (size_t)W3 * tpad3 * 4;
+            if (rings3 + 16 * per_row3 <= LDS) {
+                const uint32_t fit = (uint32_t)((LDS - rings3) / per_row3);
+                const uint32_t steps16 = (rows + 15) / 16, cap = std::max(1u, 256 / ranges);
+                const uint32_t per_wg = (steps16 + cap - 1) / cap;
+                uint32_t wgs = std::max((steps16 + per_wg - 1) / per_wg, (rows + fit - 1) / fit);
+                wgs = std::min(wgs, rows / 16);
+                const uint32_t rpw = (rows + wgs - 1) / wgs;
+                if (rpw <= fit && (uint64_t)rpw * stride <= 0xffffffffull) {
+                    const size_t lds = rings3 + rpw * per_row3;
+                    hipLaunchKernelGGL((verify_dma_kernel<ENC, 3, _Float16, 1, 1, 1>), dim3(wgs, ranges), dim3(64 * W3),
+                                       lds, s, w, stride, rows, nblocks_all, (const _Float16 *)x, in_stride, y,
+                                       out_stride, tokens, tpad3, (uint32_t)region3, (uint32_t)slot3, (uint32_t)rings3,
+                                       kb, (uint64_t)out_tokens * rows);
+                    *err = hipGetLastError();
+                    if (*err == hipSuccess && ranges > 1) {
+                        const uint32_t n = rows * out_tokens;
+                        hipLaunchKernelGGL(verify_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, scratch->work,
+                                           ranges, rows, out_tokens, y_out, out_stride_out);
+                        *err = hipGetLastError();
+                    }
+                    return true;
+                }
+            }
+        }
+    }
     const uint32_t waves = (nblocks + 1) / 2;
     const uint32_t tpad = xs3 ? 4 : (tokens + 3) & ~3u;
     const size_t slot = VDma<ENC, 2>::SLOT;

@@ -283,7 +283,9 @@ VERIFY_DMA_CASES = [(12, 17408, 5120, 8), (12, 4104, 5120, 8), (13, 1000, 4608, 
                     (12, 808, 3840, 13), (13, 12000, 6144, 16), (12, 24, 256, 1), (13, 4104, 5120, 8),
                     (12, 4096, 3840, 16), (12, 8192, 4608, 12), (12, 8192, 6144, 8),
                     # rows longer than 24 blocks: K ranges added by a second kernel
-                    (12, 5120, 17408, 8), (13, 1040, 17408, 16), (12, 2000, 12544, 5)]
+                    (12, 5120, 17408, 8), (13, 1040, 17408, 16), (12, 2000, 12544, 5),
+                    # K ranges of 17-24 Q4_K blocks: 8 waves of 3- and 2-block runs
+                    (12, 1032, 11264, 8), (12, 1032, 14080, 12), (12, 4104, 17408, 3)]
 
 
 @pytest.mark.parametrize("xdtype", ["f16", "f32"])
