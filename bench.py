@@ -14,9 +14,10 @@ HIP events on the launch stream; the roofline uses the algorithmic bytes
 
 Every other configuration runs by default with its own fixed repetition
 count (configs[0], the configs[1] down shape, the configs[2] layer step
-with its greedy token, configs[3] M=8 verify on both kernels, configs[4]
-prefill at M=512 and M=4096 on both matrices), each output checked against
-the CPU oracle (a row or token sample) before it is reported.
+with its greedy token, configs[3] M=8 verify on both kernels, the F32
+multi-token GEMV at 2, 3 and 8 token rows, configs[4] prefill at M=512 and
+M=4096 on both matrices), each output checked against the CPU oracle (a row
+or token sample) before it is reported.
 
 cpu_baseline: the CPU oracle's matvec (the C restatement of nuclis's
 cpu.matvec; the Zig reference cannot be built here) on the same matrix, timed
@@ -444,6 +445,11 @@ def main():
                            kernel=nq.KERNEL_AUTO, x_f16=False, check=(orc, np.arange(tokens), 4e-6))
             d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]
             configs[f"multi-token T={tokens} f32 q4_k gate 17408x5120 (auto route)"] = d
+        # matvecRows at its largest token count (F32, passes of 3 + 3 + 2 tokens)
+        d = bench_gemm(torch, nq, backend, stream, e, r, c, 8, reps=100, warmup=10, w_seed=sd, x_seed=4,
+                       kernel=nq.KERNEL_ROWS, x_f16=False, check=(orc, np.arange(8), 4e-6))
+        d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]
+        configs["multi-token T=8 f32 q4_k gate 17408x5120 (matvecRows)"] = d
     prefill = None
     if want("prefill"):
         e, r, c, sd = CONFIGS["c5_gate"]
