@@ -57,3 +57,31 @@ def test_random_shape_matmul_matches_oracle(backend, encoding, rows, columns, to
     # activations (and some weights) to f16
     k = F32_K if xdtype == "f32" and tokens <= 3 else F16_K
     check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, f"random {encoding}")
+
+
+def gemv_cases(n=24, seed=77):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        enc = int(rng.choice(ENCODINGS))
+        block = 32 if enc == 8 else 256
+        rows = int(rng.integers(1, 9000))
+        columns = int(rng.integers(1, 80)) * block
+        out.append((enc, rows, columns, int(rng.integers(1 << 20))))
+    return out
+
+
+@pytest.mark.parametrize("encoding,rows,columns,seed", gemv_cases())
+def test_random_shape_matvec_matches_oracle(backend, encoding, rows, columns, seed):
+    """The decode GEMV (any row count, any whole-block width) against the
+    oracle at the plain F32 bound."""
+    import torch
+    print(f"[random-gemv] enc {encoding} {rows}x{columns} seed {seed}", flush=True)
+    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+    x = gaussian(seed + 1, columns)
+    out = torch.full((rows,), np.nan, dtype=torch.float32, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    want = orc.matvec(encoding, rows, columns, w, x)
+    check_close(out.cpu().numpy()[None, :], want[None, :], mass(encoding, w, rows, columns, x[None, :]), F32_K,
+                f"random gemv {encoding}")
