@@ -54,7 +54,9 @@ enum nuq_dtype { NUQ_F32 = 0, NUQ_F16 = 1 };
 /* Kernels nuq_matmul_kernel may force (measurement aid). */
 enum nuq_kernel {
     NUQ_KERNEL_AUTO = 0,      /* the routing nuq_matmul uses */
-    NUQ_KERNEL_ROWS = 1,      /* register-dequant multi-token GEMV (tokens <= 8) */
+    NUQ_KERNEL_ROWS = 1,      /* multi-token GEMV at F32 precision (tokens <= 8): register
+                                 dequant; Q4_K / Q5_K on the matrix cores (F32 rows as three
+                                 f16 parts, f16 rows as they are) */
     NUQ_KERNEL_TILE = 2,      /* LDS-dequant f16 MFMA tile */
     NUQ_KERNEL_GENERIC = 3    /* one-row-per-wave F32 control, any alignment */
 };

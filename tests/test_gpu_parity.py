@@ -709,3 +709,27 @@ def test_matvec_rows_in_chunks_matches_oracle(backend, encoding, rows, columns, 
     check_close(got, want, mass(encoding, w, rows, columns, x), F32_K, f"rows-chunks {encoding}")
     assert np.array_equal(got.view(np.uint32), out2.cpu().numpy().view(np.uint32))
     assert np.array_equal(got[:first].view(np.uint32), alone.cpu().numpy().view(np.uint32))
+
+
+# f16 token rows under KERNEL_ROWS (and 1..3 of them on the automatic route)
+# run on the streamed verify tile for Q4_K / Q5_K: exact f16 activations
+# times exact f16 integers q * sc, so the plain F32 bound holds.
+@pytest.mark.parametrize("encoding,rows,columns", [(12, 2056, 5120), (13, 1040, 5120), (12, 1040, 17408)])
+@pytest.mark.parametrize("tokens", [2, 3, 8])
+def test_matvec_rows_f16_matches_oracle(backend, encoding, rows, columns, tokens):
+    import torch
+    w = quantized(encoding, rows, columns, 140 + tokens)
+    x16 = gaussian(141 + tokens, (tokens, columns)).astype(np.float16)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    xg = to_gpu(x16)
+    print(f"[rows-f16] enc {encoding} {rows}x{columns} T={tokens}", flush=True)
+    out = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, out, rows, tokens)
+    auto = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matmul(m, xg, columns, auto, rows, tokens)
+    backend.sync()
+    x = x16.astype(np.float32)
+    want = orc.matmul(encoding, rows, columns, w, x)
+    got = out.cpu().numpy()
+    check_close(got, want, mass(encoding, w, rows, columns, x), F32_K, f"rows-f16 {encoding}")
+    assert np.array_equal(got.view(np.uint32), auto.cpu().numpy().view(np.uint32))
