@@ -85,3 +85,48 @@ def test_random_shape_matvec_matches_oracle(backend, encoding, rows, columns, se
     want = orc.matvec(encoding, rows, columns, w, x)
     check_close(out.cpu().numpy()[None, :], want[None, :], mass(encoding, w, rows, columns, x[None, :]), F32_K,
                 f"random gemv {encoding}")
+
+
+def strided_cases(n=14, seed=4242):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        enc = int(rng.choice(ENCODINGS))
+        tokens = int(rng.choice(TOKENS[1:] + [200, 257]))
+        rows = int(rng.integers(2, 400)) * 8
+        columns = int(rng.integers(1, 33)) * 256
+        if rows * columns * tokens > 1.0e9:
+            continue
+        xdtype = str(rng.choice(["f16", "f32"]))
+        pad_in, pad_out = 8 * int(rng.integers(1, 9)), int(rng.integers(1, 40))
+        out.append((enc, rows, columns, tokens, xdtype, pad_in, pad_out, int(rng.integers(1 << 20))))
+    # the F32 multi-token form (2-3 tokens, one range and K ranges), IQ4_XS,
+    # and an F32 prefill
+    out += [(12, 1040, 5120, 2, "f32", 8, 5, 11), (13, 528, 17408, 3, "f32", 16, 3, 12),
+            (23, 640, 2560, 8, "f16", 8, 7, 13), (23, 512, 4096, 257, "f16", 24, 9, 14),
+            (12, 1024, 5120, 300, "f32", 32, 8, 15)]
+    return out
+
+
+@pytest.mark.parametrize("encoding,rows,columns,tokens,xdtype,pad_in,pad_out,seed", strided_cases())
+def test_random_strided_matmul_matches_oracle(backend, encoding, rows, columns, tokens, xdtype, pad_in, pad_out,
+                                              seed):
+    """Activation rows wider than the matrix (in_stride > columns) and output
+    rows wider than its row count (out_stride > rows): the products match the
+    oracle and the padding of every output row stays untouched."""
+    import torch
+    in_stride, out_stride = columns + pad_in, rows + pad_out
+    print(f"[random-strided] enc {encoding} {rows}x{columns} tokens {tokens} {xdtype} "
+          f"in_stride {in_stride} out_stride {out_stride} seed {seed}", flush=True)
+    w = nq.quantize(encoding, gaussian(seed, (rows, columns), 0.02))
+    x32 = gaussian(seed + 1, (tokens, in_stride))
+    xref = x32[:, :columns].astype(np.float16).astype(np.float32) if xdtype == "f16" else x32[:, :columns]
+    xg = to_gpu(x32.astype(np.float16)) if xdtype == "f16" else to_gpu(x32)
+    out = torch.full((tokens, out_stride), np.nan, dtype=torch.float32, device="cuda")
+    backend.matmul(nq.Matrix(encoding, rows, columns, to_gpu(w)), xg, in_stride, out, out_stride, tokens)
+    backend.sync()
+    got = out.cpu().numpy()
+    assert np.isnan(got[:, rows:]).all(), "output padding was written"
+    want = orc.matmul(encoding, rows, columns, w, np.ascontiguousarray(xref))
+    k = F32_K if xdtype == "f32" and tokens <= 3 else F16_K
+    check_close(got[:, :rows], want, mass(encoding, w, rows, columns, xref), k, f"strided {encoding}")
