@@ -314,13 +314,26 @@ template <uint32_t ENC>
 struct WRaw;
 template <>
 struct WRaw<12> {
-    uint4 hdr, qs;
+    u32x4 hdr, qs;
     float mul0, off0, mul1, off1;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(ks >> 2) * 144;
-        hdr = *(const uint4 *)blk;
-        qs = *(const uint4 *)(blk + 16 + (ks & 3) * 32 + part * 16);
+        hdr = *(const u32x4 *)blk;
+        qs = *(const u32x4 *)(blk + 16 + (ks & 3) * 32 + part * 16);
     }
+    // The same two loads as asm, which the compiler does not track: the
+    // caller waits with wait<N>(), N = vector memory ops issued after them.
+    __device__ __forceinline__ void load_asm(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 144;
+        const uint8_t *q = blk + 16 + (ks & 3) * 32 + part * 16;
+        asm volatile("global_load_dwordx4 %0, %2, off\n\tglobal_load_dwordx4 %1, %3, off"
+                     : "=&v"(hdr), "=&v"(qs) : "v"(blk), "v"(q) : "memory");
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%2)" : "+v"(hdr), "+v"(qs) : "n"(N) : "memory");
+    }
+
     __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
         if (c == 0) {
             const uint32_t p = ks & 3;
@@ -493,6 +506,15 @@ constexpr int PF_BM = 256, PF_BN = 256, PF_GROUP_M = 4;
 #define NUQ_PF_COPY_FIRST_MASK ((1u << 8) | (1u << 13) | (1u << 14))
 #endif
 template <uint32_t ENC> struct PF_COPY_FIRST { static constexpr bool value = (NUQ_PF_COPY_FIRST_MASK >> (ENC & 31)) & 1u; };
+// Q4_K weight prefetch as asm loads the compiler does not track (f16
+// activations, copy-first order): the step's end then waits for the
+// activation copies only, and the weights keep their two-step distance. The
+// compiler's own waits fall back to vmcnt(0) behind the LDS copies. Q4_K at
+// M=512: 562-569 -> 585-589 TFLOP/s; M=4096 unchanged (848-861 -> 857-858).
+template <uint32_t ENC, typename XT> struct PF_ASMW {
+    static constexpr bool value = ENC == 12 && sizeof(XT) == 2;
+    static constexpr int LOADS = 2;  // WRaw<12>::load_asm's instructions
+};
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
@@ -652,14 +674,17 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
         }
     if (ksteps > 1) {
 #pragma unroll
-        for (uint32_t s_ = 0; s_ < SP; ++s_) wA[s_].load(wrow, 1, NUQ_PF_PART(s_));
+        for (uint32_t s_ = 0; s_ < SP; ++s_) {
+            if constexpr (PF_ASMW<ENC, XT>::value) wA[s_].load_asm(wrow, 1, NUQ_PF_PART(s_));
+            else wA[s_].load(wrow, 1, NUQ_PF_PART(s_));
+        }
     }
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __syncthreads();
 
     // One K step; a macro rather than a lambda so the accumulators stay in
     // registers (a capturing lambda takes their address).
-#define NUQ_PF_STEP(KS, WNEXT, WFAR)                                                                               \
+#define NUQ_PF_STEP(KS, WNEXT, WFAR, WAITN)                                                                        \
     {                                                                                                              \
         const uint32_t ks_ = (KS);                                                                                 \
         const uint32_t cur = ks_ & 1;                                                                              \
@@ -672,7 +697,7 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
         _Pragma("unroll") for (int j = 0; j < (int)TJ; ++j) fb[0][j] = *(const half8 *)(wb + j * 32 * LDS_PITCH);  \
         const bool far_ = ks_ + 2 < ksteps;                                                                        \
         /* PF_COPY_FIRST: the activation copy is issued before the weight prefetch */                            \
-        if (!PF_COPY_FIRST<ENC>::value && far_) {                                                                  \
+        if (!(PF_COPY_FIRST<ENC>::value || PF_ASMW<ENC, XT>::value) && far_) {                                    \
             _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) WFAR[s_].load(wrow, ks_ + 2, NUQ_PF_PART(s_));  \
         }                                                                                                          \
         if (next) {                                                                                                \
@@ -683,8 +708,19 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
                     xr[s_].load(xrow + slab_chunk_col<ENC>(4 * NUQ_PF_PART(s_)) + slab_k0<ENC>(ks_ + 1), xvalid);  \
             }                                                                                                      \
         }                                                                                                          \
-        if (PF_COPY_FIRST<ENC>::value && far_) {                                                                   \
-            _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) WFAR[s_].load(wrow, ks_ + 2, NUQ_PF_PART(s_));  \
+        if ((PF_COPY_FIRST<ENC>::value || PF_ASMW<ENC, XT>::value) && far_) {                                     \
+            /* the weight loads stay behind the copies, so the step's end can wait for the copies alone */         \
+            asm volatile("" ::: "memory");                                                                         \
+            __builtin_amdgcn_sched_barrier(0);                                                                     \
+            _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) {                                               \
+                if constexpr (PF_ASMW<ENC, XT>::value) WFAR[s_].load_asm(wrow, ks_ + 2, NUQ_PF_PART(s_));          \
+                else WFAR[s_].load(wrow, ks_ + 2, NUQ_PF_PART(s_));                                                \
+            }                                                                                                      \
+        }                                                                                                          \
+        if constexpr (PF_ASMW<ENC, XT>::value) {                                                                   \
+            /* the previous step's weight loads are older than this step's copies and loads (WAITN of them at */  \
+            /* least) */                                                                                           \
+            _Pragma("unroll") for (uint32_t s_ = 0; s_ < SP; ++s_) WNEXT[s_].template wait<WAITN>();               \
         }                                                                                                          \
         _Pragma("unroll") for (uint32_t kk = 0; kk < BK / 16; ++kk) {                                              \
             const uint32_t p_ = kk & 1;                                                                            \
@@ -713,20 +749,41 @@ __global__ void __launch_bounds__(64 * NW) prefill_kernel(const uint8_t *__restr
                 _Pragma("unroll") for (uint32_t c = 0; c < 4; ++c) xr[s_].store(xdst, c);                          \
             }                                                                                                      \
         }                                                                                                          \
-        if (DMA && PF_COPY_FIRST<ENC>::value) {                                                                    \
+        if (DMA && (PF_COPY_FIRST<ENC>::value || PF_ASMW<ENC, XT>::value)) {                                      \
             /* this step's copies have landed and the dequantised weights are written; the barrier */             \
             /* carries no fence */                                                                                \
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");                                         \
+            if (PF_ASMW<ENC, XT>::value && far_) /* the weight loads may stay in flight */                         \
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(SP * PF_ASMW<ENC, XT>::LOADS) : "memory");   \
+            else                                                                                                   \
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");                                     \
             __builtin_amdgcn_s_barrier();                                                                          \
         } else {                                                                                                   \
             if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70); /* vmcnt(0): this step's DMA has landed */     \
             __syncthreads();                                                                                       \
         }                                                                                                          \
     }
-    for (uint32_t ks = 0; ks < ksteps; ++ks) {
-        NUQ_PF_STEP(ks, wA, wB)
+    if constexpr (PF_ASMW<ENC, XT>::value) {
+        // Two steps per iteration, the register sets trading roles (no copy
+        // of registers an untracked load may still be filling). Every step of
+        // the loop issues at least XD_INSTRS / NW activation copies per wave
+        // and then its two weight loads, all younger than the previous step's
+        // weight loads: waiting for all but YOUNG of them leaves those landed.
+        // The last one to three steps wait for everything.
+        constexpr int YOUNG = XD_INSTRS / NW + PF_ASMW<ENC, XT>::LOADS * SP;
+        uint32_t ks = 0;
+        for (; ks + 3 < ksteps; ks += 2) {
+            NUQ_PF_STEP(ks, wA, wB, YOUNG)
+            NUQ_PF_STEP(ks + 1, wB, wA, YOUNG)
+        }
+        if (ks < ksteps) NUQ_PF_STEP(ks, wA, wB, 0)
+        if (ks + 1 < ksteps) NUQ_PF_STEP(ks + 1, wB, wA, 0)
+        if (ks + 2 < ksteps) NUQ_PF_STEP(ks + 2, wA, wB, 0)
+    } else {
+        for (uint32_t ks = 0; ks < ksteps; ++ks) {
+            NUQ_PF_STEP(ks, wA, wB, 0)
 #pragma unroll
-        for (uint32_t s_ = 0; s_ < SP; ++s_) wA[s_] = wB[s_];
+            for (uint32_t s_ = 0; s_ < SP; ++s_) wA[s_] = wB[s_];
+        }
     }
 #undef NUQ_PF_STEP
 #undef NUQ_PF_PART
