@@ -753,7 +753,8 @@ constexpr int gd_threads() { return ENC == 14 ? 768 : GI_WG_THREADS; }
 // form is straight-line code: the asm loads' registers must not be touched
 // before their explicit waits, and a branch merging two forms made the
 // compiler copy them early).
-template <uint32_t ENC, int SLOTS, int D, bool TWO = false>
+// WX: every wave quantises its own blocks' x slices (one wave set).
+template <uint32_t ENC, int SLOTS, int D, bool TWO = false, bool WX = false>
 __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
                                                                       uint32_t rows, uint32_t nblocks,
                                                                       uint32_t rows_per_wg, uint32_t set_waves,
@@ -853,6 +854,31 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     const uint32_t first_local = first - row_begin, last_local = row_end - 1 - row_begin;
 
     const uint32_t t0 = threadIdx.x;
+    if constexpr (WX) {
+        // Each wave quantises the slices of its own blocks (SLOTS / 4 rounds
+        // of one half-slice per lane) and reads them back after its own LDS
+        // writes: no workgroup barrier before the steps. Taken with one wave
+        // set (gd_wave_x); with several, each set would quantise all of x
+        // again (17408 x 5120 took 14.7 against 13.1-13.3 us).
+        constexpr uint32_t R = SLOTS / 4;
+        const uint32_t hbase = 16 * SLOTS * kw, hend = 2 * nslices;
+        XHalf xr[R];
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint32_t h = min(hbase + 64 * r + lane, hend - 1);
+            load_half_slice_asm(x + (uint64_t)(h >> 1) * 32, h & 1, xr[r]);
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) NUQ_GD_DMA(d, (uint32_t)d)
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint32_t h = hbase + 64 * r + lane;
+            if (r == 0) xhalf_wait<GD_DMA_INSTRS * D + 4 * (R - 1)>(xr[r]);
+            else xhalf_wait<GD_DMA_INSTRS * D>(xr[r]);
+            if (h < hend) quantize_half_slice<true>(xr[r], h & 1, slices + (h >> 1) * SLICE_WORDS);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    } else {
     XHalf xh;
     if (t0 < 2 * nslices) load_half_slice_asm(x + (uint64_t)(t0 >> 1) * 32, t0 & 1, xh);
     // When x takes a second round of half-slices (long rows: 1088 for
@@ -888,6 +914,7 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     }
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     __builtin_amdgcn_s_barrier();
+    }
 
     XSlice xa, xb;
     const uint32_t bb = live ? b : 0;
@@ -950,6 +977,12 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     }
 }
 
+// Wave-local x quantisation (the kernel's WX form) where it measured faster
+// with one wave set: 8-block lane groups of Q4_K (5120 x 17408: 15.8 -> 15.4 us,
+// mean of 4 A/B pairs) and Q6_K (21.3 -> 21.1); Q5_K was 1 % slower.
+template <uint32_t ENC, int SLOTS>
+constexpr bool gd_wave_x() { return SLOTS == 8 && (ENC == 12 || ENC == 14); }
+
 template <uint32_t ENC, int SLOTS, int D>
 static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks,
                                  const float *x, float *y, uint32_t sets_wanted, uint32_t wgs_per_cu,
@@ -986,6 +1019,13 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return hipErrorInvalidValue;  // 32-bit copy offsets
     const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg + (tail ? 1 : 0)), block(64 * waves);
+    if constexpr (gd_wave_x<ENC, SLOTS>()) {
+        if (sets == 1) {  // each wave quantises its own slices
+            hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, false, true>), grid, block, lds, s, w, stride, rows,
+                               nblocks, rows_per_wg, set_waves, x, y, tail ? 1u : 0u, GdSegments{});
+            return hipGetLastError();
+        }
+    }
     if (2 * nblocks * 8 > 64 * waves)  // x in two rounds of half-slices (or more)
         hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, true>), grid, block, lds, s, w, stride, rows, nblocks,
                            rows_per_wg, set_waves, x, y, tail ? 1u : 0u, GdSegments{});
@@ -1037,6 +1077,13 @@ static hipError_t launch_dma_segments(hipStream_t s, uint32_t count, const uint8
     while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
     const size_t lds = lds_for(sets);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if constexpr (gd_wave_x<ENC, SLOTS>()) {
+        if (sets == 1) {  // each wave quantises its own slices
+            hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, false, true>), dim3(wgs), dim3(64 * set_waves), lds, s,
+                               w[0], stride, rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
+            return hipGetLastError();
+        }
+    }
     if (2 * nblocks * 8 > 64 * set_waves * sets)
         hipLaunchKernelGGL((gemv_dma_kernel<ENC, SLOTS, D, true>), dim3(wgs), dim3(64 * set_waves * sets), lds, s,
                            w[0], stride, rows[0], nblocks, max_rpw, set_waves, x, y[0], 0u, segs);
