@@ -278,6 +278,7 @@ struct XLoad<float> {
 typedef _Float16 half4v_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Two f16 values 1024 + v from bytes i and j of t (each v < 1024): the
 // byte goes into the low mantissa byte of 1024.0 (0x6400, ulp 1) by one
@@ -360,9 +361,28 @@ struct WRaw<12> {
 // ql bytes, 16 qh bytes, the scales and d once for 32 values.
 template <>
 struct WRaw<14> {
-    uint4 ql, qh, sc16;
+    u32x4 ql, qh, sc16;
     uint32_t d16;
     float mul_lo, mul_hi;
+    // load() as asm (three unaligned 16-byte loads and one 2-byte load),
+    // untracked by the compiler: wait<N>() as for WRaw<12>
+    __device__ __forceinline__ void load_asm(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 210;
+        const uint32_t h = (ks & 3) >> 1, qa = ks & 1;
+        const uint8_t *pa = blk + h * 64 + qa * 32 + 16 * part, *pb = blk + 128 + h * 32 + 16 * part;
+        asm volatile(
+            "global_load_dwordx4 %0, %4, off\n\t"
+            "global_load_dwordx4 %1, %5, off\n\t"
+            "global_load_dwordx4 %2, %6, off offset:192\n\t"
+            "global_load_ushort %3, %6, off offset:208"
+            : "=&v"(ql), "=&v"(qh), "=&v"(sc16), "=&v"(d16)
+            : "v"(pa), "v"(pb), "v"(blk)
+            : "memory");
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(ql), "+v"(qh), "+v"(sc16), "+v"(d16) : "n"(N) : "memory");
+    }
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(ks >> 2) * 210;
         const uint32_t h = (ks & 3) >> 1, qa = ks & 1;
@@ -372,9 +392,9 @@ struct WRaw<14> {
         const u32x4_a2 a = *(const u32x4_a2 *)(blk + h * 64 + qa * 32 + 16 * part);
         const u32x4_a2 b = *(const u32x4_a2 *)(blk + 128 + h * 32 + 16 * part);
         const u32x4_a2 c = *(const u32x4_a2 *)(blk + 192);
-        ql = make_uint4(a.x, a.y, a.z, a.w);
-        qh = make_uint4(b.x, b.y, b.z, b.w);
-        sc16 = make_uint4(c.x, c.y, c.z, c.w);
+        ql = u32x4{a.x, a.y, a.z, a.w};
+        qh = u32x4{b.x, b.y, b.z, b.w};
+        sc16 = u32x4{c.x, c.y, c.z, c.w};
         d16 = load_u16_bytes(blk + 208);
     }
     __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
@@ -400,14 +420,30 @@ struct WRaw<14> {
 };
 template <>
 struct WRaw<13> {
-    uint4 hdr, qh, qs;
+    u32x4 hdr, qh, qs;
     uint32_t p2;  // 2 * pair: the high-plane bit of the low-nibble group
     float mul0, off0, mul1, off1;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(ks >> 2) * 176;
-        hdr = *(const uint4 *)blk;
-        qh = *(const uint4 *)(blk + 16 + part * 16);
-        qs = *(const uint4 *)(blk + 48 + (ks & 3) * 32 + part * 16);
+        hdr = *(const u32x4 *)blk;
+        qh = *(const u32x4 *)(blk + 16 + part * 16);
+        qs = *(const u32x4 *)(blk + 48 + (ks & 3) * 32 + part * 16);
+    }
+    // load() as asm, untracked by the compiler: wait<N>() as for WRaw<12>
+    __device__ __forceinline__ void load_asm(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 176;
+        const uint8_t *ph = blk + 16 + part * 16, *pq = blk + 48 + (ks & 3) * 32 + part * 16;
+        asm volatile(
+            "global_load_dwordx4 %0, %3, off\n\t"
+            "global_load_dwordx4 %1, %4, off\n\t"
+            "global_load_dwordx4 %2, %5, off"
+            : "=&v"(hdr), "=&v"(qh), "=&v"(qs)
+            : "v"(blk), "v"(ph), "v"(pq)
+            : "memory");
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(hdr), "+v"(qh), "+v"(qs) : "n"(N) : "memory");
     }
     __device__ __forceinline__ void dequant(uint32_t ks, uint32_t part, uint32_t c, _Float16 *out) {
         if (c == 0) {
@@ -442,14 +478,30 @@ struct WRaw<13> {
 };
 template <>
 struct WRaw<23> {
-    uint2 hdr, q01, q23;  // d, scales_h, scales_l; the group's 16 code bytes
+    u32x2 hdr, q01, q23;  // d, scales_h, scales_l; the group's 16 code bytes
     float mul;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(ks >> 2) * 136;
         const uint32_t g = 2 * (ks & 3) + part;
-        hdr = *(const uint2 *)blk;
-        q01 = *(const uint2 *)(blk + 8 + 16 * g);
-        q23 = *(const uint2 *)(blk + 16 + 16 * g);
+        hdr = *(const u32x2 *)blk;
+        q01 = *(const u32x2 *)(blk + 8 + 16 * g);
+        q23 = *(const u32x2 *)(blk + 16 + 16 * g);
+    }
+    // load() as asm, untracked by the compiler: wait<N>() as for WRaw<12>
+    __device__ __forceinline__ void load_asm(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(ks >> 2) * 136;
+        const uint8_t *pq = blk + 8 + 16 * (2 * (ks & 3) + part);
+        asm volatile(
+            "global_load_dwordx2 %0, %3, off\n\t"
+            "global_load_dwordx2 %1, %4, off\n\t"
+            "global_load_dwordx2 %2, %4, off offset:8"
+            : "=&v"(hdr), "=&v"(q01), "=&v"(q23)
+            : "v"(blk), "v"(pq)
+            : "memory");
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(hdr), "+v"(q01), "+v"(q23) : "n"(N) : "memory");
     }
     // this thread owns group 2(ks&3) + part: chunk c = byte dword c, values
     // 4c..4c+3 (low nibbles) and 16+4c.. (high nibbles)
@@ -478,42 +530,66 @@ struct WRaw<23> {
 };
 template <>
 struct WRaw<8> {
-    uint32_t q[8];
+    u32x4 qa, qb;  // the block's 32 codes
     uint32_t d16;
     __device__ __forceinline__ void load(const uint8_t *row, uint32_t ks, uint32_t part) {
         const uint8_t *blk = row + (uint64_t)(2 * ks + part) * 34;
+        // 2-byte aligned blocks: unaligned 16-byte loads (ROCm runs global
+        // memory in unaligned mode)
+        typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
         d16 = load_u16_bytes(blk);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = load_u32_unaligned(blk + 2 + 4 * k);
+        const u32x4_a2 a = *(const u32x4_a2 *)(blk + 2), b = *(const u32x4_a2 *)(blk + 18);
+        qa = u32x4{a.x, a.y, a.z, a.w};
+        qb = u32x4{b.x, b.y, b.z, b.w};
+    }
+    // load() as asm, untracked by the compiler: wait<N>() as for WRaw<12>
+    __device__ __forceinline__ void load_asm(const uint8_t *row, uint32_t ks, uint32_t part) {
+        const uint8_t *blk = row + (uint64_t)(2 * ks + part) * 34;
+        asm volatile(
+            "global_load_ushort %0, %3, off\n\t"
+            "global_load_dwordx4 %1, %3, off offset:2\n\t"
+            "global_load_dwordx4 %2, %3, off offset:18"
+            : "=&v"(d16), "=&v"(qa), "=&v"(qb)
+            : "v"(blk)
+            : "memory");
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(d16), "+v"(qa), "+v"(qb) : "n"(N) : "memory");
     }
     __device__ __forceinline__ void dequant(uint32_t, uint32_t part, uint32_t c, _Float16 *out) {
         const float d = half_bits(d16);
+        const uint32_t w0 = c == 0 ? qa.x : c == 1 ? qa.z : c == 2 ? qb.x : qb.z;
+        const uint32_t w1 = c == 0 ? qa.y : c == 1 ? qa.w : c == 2 ? qb.y : qb.w;
         half8 v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (_Float16)(d * (float)(int8_t)((q[2 * c + e / 4] >> (8 * (e & 3))) & 0xff));
+        for (int e = 0; e < 8; ++e) v[e] = (_Float16)(d * (float)(int8_t)(((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 0xff));
         *(half8 *)(out + part * 32 + 8 * c) = v;
     }
 };
 
 constexpr int PF_BM = 256, PF_BN = 256, PF_GROUP_M = 4;
 
-// Step order per encoding, measured at M = 4096 on 17408x5120 and
-// 5120x17408: issuing the activation copy before the weight prefetch and
-// ending the step with explicit waits and a fence-free barrier gains 8 %
-// (Q8_0), 7 % (Q6_K) and 2 % (Q5_K); Q4_K and IQ4_XS lose 2-2.5 % and keep
-// the prefetch-first order with __syncthreads. Bit e of the mask is encoding e.
+// Step order per encoding with F32 activations (f16 activations always copy
+// first, see PF_ASMW): the activation loads before the weight prefetch for
+// Q8_0, Q5_K and Q6_K, after it for Q4_K and IQ4_XS, as measured with the
+// f16 copies before the weight loads left the compiler's tracking (8 %, 2 %,
+// 7 % gained; 2-2.5 % lost). Bit e of the mask is encoding e.
 #ifndef NUQ_PF_COPY_FIRST_MASK
 #define NUQ_PF_COPY_FIRST_MASK ((1u << 8) | (1u << 13) | (1u << 14))
 #endif
 template <uint32_t ENC> struct PF_COPY_FIRST { static constexpr bool value = (NUQ_PF_COPY_FIRST_MASK >> (ENC & 31)) & 1u; };
-// Q4_K weight prefetch as asm loads the compiler does not track (f16
-// activations, copy-first order): the step's end then waits for the
-// activation copies only, and the weights keep their two-step distance. The
-// compiler's own waits fall back to vmcnt(0) behind the LDS copies. Q4_K at
-// M=512: 562-569 -> 585-589 TFLOP/s; M=4096 unchanged (848-861 -> 857-858).
+// With f16 activations the weight prefetch is asm loads the compiler does
+// not track, issued after the activation copies: the step's end then waits
+// for the copies only and the weights keep their two-step distance (the
+// compiler's own waits fall back to vmcnt(0) behind LDS copies). A/B on one
+// box, M=4096 / M=512 TFLOP/s: Q4_K 848-861 -> 857-858 / 562-569 -> 585-589,
+// Q6_K 779-781 -> 807-809 / 577-591 -> 588-601, Q5_K 794-806 -> 844-850 /
+// 606-614 -> 630-637, IQ4_XS 850-860 -> 870-881 / 614-629 -> 652-670, Q8_0
+// 860-863 -> 880-892 / 599-616 -> 639-653.
 template <uint32_t ENC, typename XT> struct PF_ASMW {
-    static constexpr bool value = ENC == 12 && sizeof(XT) == 2;
-    static constexpr int LOADS = 2;  // WRaw<12>::load_asm's instructions
+    static constexpr bool value = sizeof(XT) == 2;
+    static constexpr int LOADS = ENC == 14 ? 4 : ENC == 12 ? 2 : 3;  // WRaw<ENC>::load_asm's instructions
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
