@@ -42,7 +42,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
 MALL_BYTES = 256 << 20
-GEMV_KERNEL = "gemv_dma_kernel<12, 4, 2>"
+GEMV_KERNEL = "gemv_dma_kernel<12, 4, 2, false, false>"
 GEMV_DTYPE = ("q4_k codes x f32 activations carried as 24-bit fixed point per 32-value slice "
               "(three int8 byte planes, exact int32 dot; F32-mantissa precision) -> f32 scale/accumulate")
 
