@@ -241,6 +241,9 @@ def check_gemv(orc, g, encoding, rows, columns, stride_rows=97):
             "worst_err_over_mass": float((err / m).max())}
 
 
+MATVEC_ROWS = "matvec_rows"  # bench_gemm's `kernel` for nuq_matvec_rows (F32 activations)
+
+
 def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps=20, warmup=3, w_seed=2,
                x_seed=5, kernel=None, check=None, x_f16=True):
     """`reps` launches of the matmul entry point (one kernel route) on
@@ -255,14 +258,21 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
     mats = [nq.Matrix(encoding, rows, columns, wg if i == 0 else wg.clone()) for i in range(copies_for(w.nbytes))]
     y = torch.full((tokens, rows), float("nan"), device="cuda")
     k = nq.KERNEL_AUTO if kernel is None else kernel
+
+    def call(m):
+        if k == MATVEC_ROWS:
+            backend.matvec_rows(m, x, columns, y, rows, tokens)
+        else:
+            backend.matmul_kernel(k, m, x, columns, y, rows, tokens)
+
     stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
         for i in range(warmup):
-            backend.matmul_kernel(k, mats[i % len(mats)], x, columns, y, rows, tokens)
+            call(mats[i % len(mats)])
         torch.cuda.synchronize()
         with Timer(torch, stream) as t:
             for i in range(reps):
-                backend.matmul_kernel(k, mats[i % len(mats)], x, columns, y, rows, tokens)
+                call(mats[i % len(mats)])
         torch.cuda.synchronize()
     s = t.ms / 1e3 / reps
     flops = 2.0 * tokens * rows * columns
@@ -433,12 +443,15 @@ def main():
         configs["configs[2] layer step + q6_k lm_head"] = bench_layer(torch, nq, backend, stream, check=orc)
         e, r, c, sd = CONFIGS["c2_gate"]
         e2, r2, c2, sd2 = CONFIGS["c2_down"]
-        # (KERNEL_ROWS with f16 activations takes this same tile for Q4_K)
-        for label, (ee, rr, cc, ss) in (("gate 17408x5120", (e, r, c, sd)), ("down 5120x17408", (e2, r2, c2, sd2))):
-            d = bench_gemm(torch, nq, backend, stream, ee, rr, cc, 8, reps=200, warmup=20, w_seed=ss, x_seed=4,
-                           kernel=nq.KERNEL_TILE, check=(orc, np.arange(8), 2e-4))
-            d["algo_gbs"] = (rr * cc // 256 * 144 + 8 * cc * 2 + 8 * rr * 4) / d["ms"] / 1e6
-            configs[f"configs[3] verify M=8 q4_k {label} tile"] = d
+        # the register-dequant multi-row GEMV (KERNEL_ROWS, F32 arithmetic)
+        # against the MFMA tile, both on f16 activations
+        for kname, kid in (("rows", nq.KERNEL_ROWS), ("tile", nq.KERNEL_TILE)):
+            for label, (ee, rr, cc, ss) in (("gate 17408x5120", (e, r, c, sd)), ("down 5120x17408", (e2, r2, c2, sd2))):
+                d = bench_gemm(torch, nq, backend, stream, ee, rr, cc, 8, reps=100 if kname == "rows" else 200,
+                               warmup=20, w_seed=ss, x_seed=4, kernel=kid,
+                               check=(orc, np.arange(8), 4e-6 if kname == "rows" else 2e-4))
+                d["algo_gbs"] = (rr * cc // 256 * 144 + 8 * cc * 2 + 8 * rr * 4) / d["ms"] / 1e6
+                configs[f"configs[3] verify M=8 q4_k {label} {kname}"] = d
         # the routed multi-token GEMV (T = 2, 3 F32 token rows, matvecRows)
         for tokens in (2, 3):
             d = bench_gemm(torch, nq, backend, stream, e, r, c, tokens, reps=200, warmup=20, w_seed=sd, x_seed=4,
@@ -447,7 +460,7 @@ def main():
             configs[f"multi-token T={tokens} f32 q4_k gate 17408x5120 (auto route)"] = d
         # matvecRows at its largest token count (F32, passes of 3 + 3 + 2 tokens)
         d = bench_gemm(torch, nq, backend, stream, e, r, c, 8, reps=100, warmup=10, w_seed=sd, x_seed=4,
-                       kernel=nq.KERNEL_ROWS, x_f16=False, check=(orc, np.arange(8), 4e-6))
+                       kernel=MATVEC_ROWS, x_f16=False, check=(orc, np.arange(8), 4e-6))
         d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]
         configs["multi-token T=8 f32 q4_k gate 17408x5120 (matvecRows)"] = d
     prefill = None

@@ -54,9 +54,7 @@ enum nuq_dtype { NUQ_F32 = 0, NUQ_F16 = 1 };
 /* Kernels nuq_matmul_kernel may force (measurement aid). */
 enum nuq_kernel {
     NUQ_KERNEL_AUTO = 0,      /* the routing nuq_matmul uses */
-    NUQ_KERNEL_ROWS = 1,      /* multi-token GEMV at F32 precision (tokens <= 8): register
-                                 dequant; Q4_K / Q5_K on the matrix cores (F32 rows as three
-                                 f16 parts, f16 rows as they are) */
+    NUQ_KERNEL_ROWS = 1,      /* register-dequant multi-token GEMV (tokens <= 8) */
     NUQ_KERNEL_TILE = 2,      /* LDS-dequant f16 MFMA tile */
     NUQ_KERNEL_GENERIC = 3    /* one-row-per-wave F32 control, any alignment */
 };
@@ -133,8 +131,9 @@ int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint6
 
 /* Backend.matmul (ops/matmul.zig:62-108): any token count; x is F32 or F16
  * ([tokens][in_stride] elements). Routes: tokens == 1 -> GEMV, tokens <= 3
- * -> multi-token GEMV, otherwise the f16 MFMA tile. Requires rows % 8 == 0
- * and columns % 64 == 0 as the reference does. */
+ * -> multi-token GEMV (F16 x on Q4_K / Q5_K: the verify tile, exact in its
+ * products), otherwise the f16 MFMA tile. Requires rows % 8 == 0 and
+ * columns % 64 == 0 as the reference does. */
 int nuq_matmul(nuq_context *ctx, const nuq_matrix *m, const void *x, uint32_t x_dtype, uint64_t in_stride, float *out,
                uint64_t out_stride, uint32_t tokens);
 /* Backend.matmulKernel (ops/matmul.zig:73-75): same contract, forcing a

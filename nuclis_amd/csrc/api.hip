@@ -252,17 +252,16 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
             const int r = run_rows_mfma(ctx, m, stride, (const float *)x, in_stride, out, out_stride, tokens);
             if (r >= 0) return r;
         }
-        kernel = tokens <= 3 && specialised(m->encoding) ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
-    } else if (kernel == NUQ_KERNEL_ROWS && !f16 && tokens >= 2) {
-        const int r = run_rows_mfma(ctx, m, stride, (const float *)x, in_stride, out, out_stride, tokens);
-        if (r >= 0) return r;
+        // F16 activations on Q4_K / Q5_K take the streamed verify tile: it
+        // multiplies the exact f16 activations by the exact f16 integers
+        // q * sc and applies d and the minima in F32, so every product is
+        // exact and the register GEMV's F32 precision holds while the
+        // weights stream once for all tokens.
+        const bool exact_tile = f16 && (m->encoding == NUQ_Q4_K || m->encoding == NUQ_Q5_K);
+        kernel = tokens <= 3 && specialised(m->encoding) && !exact_tile ? NUQ_KERNEL_ROWS : NUQ_KERNEL_TILE;
     }
-    // F16 activations on Q4_K / Q5_K: the streamed verify tile multiplies the
-    // exact f16 activations by the exact f16 integers q * sc and applies d and
-    // the minima in F32, so every product is exact and it keeps the register
-    // GEMV's F32 precision while streaming the weights once for all tokens.
-    if (kernel == NUQ_KERNEL_ROWS && f16 && (m->encoding == NUQ_Q4_K || m->encoding == NUQ_Q5_K))
-        kernel = NUQ_KERNEL_TILE;
+    // NUQ_KERNEL_ROWS forces the register-dequant multi-row GEMV (a
+    // measurement aid, as the reference's matmulKernel forces a kernel).
     if (kernel == NUQ_KERNEL_ROWS && !specialised(m->encoding))
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
     if (kernel == NUQ_KERNEL_ROWS)

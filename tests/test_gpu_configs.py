@@ -4,8 +4,8 @@ CPU oracle.
 
   configs[0]  Q8_0 4096 x 4096 GEMV, W seed 0, x seed 1
   configs[1]  Q4_K GEMV 17408 x 5120 (gate/up) and 5120 x 17408 (down)
-  configs[3]  M=8 verify on both Q4_K matrices through KERNEL_ROWS (F32
-              bound) and KERNEL_TILE (the half-tile bound)
+  configs[3]  M=8 verify on both Q4_K matrices: the register GEMV
+              (KERNEL_ROWS) and the MFMA tile (KERNEL_TILE)
   configs[4]  prefill at M=512 and M=4096: Q4_K 17408 x 5120 and
               Q6_K 5120 x 17408, f16 activations
 
@@ -70,9 +70,7 @@ def test_config_verify_m8(backend, name, kernel):
     backend.sync()
     xref = x16.astype(np.float32)
     want = orc.matmul(enc, rows, cols, w, xref)
-    # KERNEL_ROWS keeps F32 precision: for Q4_K with f16 activations it runs
-    # the verify tile, whose products (exact f16 x times exact f16 q * sc)
-    # are exact
+    # the register GEMV computes in F32 (the f16 activations widen exactly)
     k = F32_K if kernel == "rows" else F16_K
     check_close(out.cpu().numpy(), want, mass(enc, w, rows, cols, xref), k, f"verify_{kernel} {name}")
 
