@@ -458,7 +458,7 @@ def main():
                            kernel=nq.KERNEL_AUTO, x_f16=False, check=(orc, np.arange(tokens), 4e-6))
             d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]
             configs[f"multi-token T={tokens} f32 q4_k gate 17408x5120 (auto route)"] = d
-        # matvecRows at its largest token count (F32, passes of 3 + 3 + 2 tokens)
+        # matvecRows at its largest token count (F32, two passes of 4 tokens)
         d = bench_gemm(torch, nq, backend, stream, e, r, c, 8, reps=100, warmup=10, w_seed=sd, x_seed=4,
                        kernel=MATVEC_ROWS, x_f16=False, check=(orc, np.arange(8), 4e-6))
         d["ratio_to_m1"] = d["ms"] * 1e3 / g["us_per_launch"]

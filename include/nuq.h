@@ -123,8 +123,8 @@ int nuq_dequant_range(nuq_context *ctx, const nuq_matrix *m, uint64_t first, uin
 int nuq_matvec(nuq_context *ctx, const nuq_matrix *m, const float *x, float *out);
 
 /* Backend.matvecRows (ops/matvec.zig:149-188): 2 <= tokens <= 8 activation
- * rows, F32 precision. Q4_K / Q5_K serve at most 3 token rows per pass over
- * the weights (4..8 rows: passes of 3 and 2); the other encodings decode each
+ * rows, F32 precision. Q4_K / Q5_K serve at most 4 token rows per pass over
+ * the weights (5..8 rows: two passes); the other encodings decode each
  * weight once and dot it with every token row. */
 int nuq_matvec_rows(nuq_context *ctx, const nuq_matrix *m, const float *x, uint64_t in_stride, float *out,
                     uint64_t out_stride, uint32_t tokens);

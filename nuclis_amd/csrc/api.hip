@@ -191,17 +191,16 @@ int run_gemv(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float
 
 // F32 activations of 2..8 tokens at F32 precision on the matrix cores
 // (Q4_K / Q5_K); returns -1 when the shape is not one it takes (nothing is
-// launched then). One launch serves at most 3 tokens, so 4..8 tokens run as
-// launches of 3 and 2 (4 = 2 + 2, 5 = 3 + 2, ..., 8 = 3 + 3 + 2): each token's
-// row sums do not depend on the others, and every launch streams the weights
-// once, which still beats the register GEMV at 8 tokens by about 2x.
+// launched then). One launch serves at most 4 tokens, so 5..8 tokens run as
+// two launches (5 = 4 + 1, ..., 8 = 4 + 4): each token's row sums do not
+// depend on the others, and every launch streams the weights once.
 int run_rows_mfma(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const float *x, uint64_t in_stride,
                   float *out, uint64_t out_stride, uint32_t tokens) {
     if (tokens < 2 || tokens > 8 || (m->encoding != NUQ_Q4_K && m->encoding != NUQ_Q5_K)) return -1;
     (void)ensure_workspace(ctx, nuq::tile_workspace_floats(m->encoding, (uint32_t)m->rows, (uint32_t)m->columns,
-                                                           std::min(tokens, 3u), in_stride, true));
+                                                           std::min(tokens, 4u), in_stride, true));
     for (uint32_t t0 = 0; t0 < tokens;) {
-        const uint32_t left = tokens - t0, c = left == 4 ? 2 : std::min(left, 3u);
+        const uint32_t c = std::min(tokens - t0, 4u);
         const hipError_t e = nuq::launch_rows_mfma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
                                                    (uint32_t)m->rows, (uint32_t)m->columns, x + t0 * in_stride,
                                                    in_stride, out + t0 * out_stride, out_stride, c, ctx->split);

@@ -1770,6 +1770,7 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
     half8 bx[NB][8];
     float sx3[NB][2], sft[4];  // XS = 3: F32 group sums; each token's scale back
     float gs3[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // XS = 3: staged group sums of this lane's token
+    u32x4 xr3[NB][8] = {};  // XS = 3: this lane's part fragments, read during the staging
     if constexpr (STAGE != 0) {
         // this wave's activations, [token][its blocks' 512 bytes], copied
         // before the step-0 weights so that they are waited for alone
@@ -1781,9 +1782,12 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         uint8_t *xs = STAGE == 1 ? (VS ? ring : ring + V::SLOT) : vd_lds + nwaves * V::SLOT + b0 * tokens * 512;
         if constexpr (XS == 3) {
             // F32 activations: lane k converts values [8k, 8k + 8) of the
-            // wave's run of each token into its three f16 parts (staging
-            // rows pT + t), the F32 sums of 32-value groups go to the lanes
-            // that need them, and the wave agrees on the token's scale 2^e
+            // wave's run of each token into its three f16 parts, the F32
+            // sums of 32-value groups go to the lanes that need them, and the
+            // wave agrees on the token's scale 2^e. Tokens go through the
+            // staging two at a time (part p of the phase's token tt at
+            // staging row 2p + tt), each lane reading its fragments in its
+            // token's phase, so four tokens stage in the room of two.
             static_assert(STAGE == 1, "F32 activations are staged in the wave's own region");
             (void)xchunks;
             (void)span_log2;
@@ -1791,9 +1795,9 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
             const bool live_k = 8 * lane < nlive * 256;
             // every token's values are loaded before the step-0 copies; lanes
             // past the run and tokens past `tokens` load valid bytes and drop them
-            float4 fl[3][2];
+            float4 fl[4][2];
 #pragma unroll
-            for (uint32_t t = 0; t < 3; ++t) {
+            for (uint32_t t = 0; t < 4; ++t) {
                 const float *src = (const float *)x + (uint64_t)min(t, tokens - 1) * in_stride + b0 * L::BLOCK_VALUES +
                                    8 * (live_k ? lane : 0);
                 fl[t][0] = *(const float4 *)src;
@@ -1802,60 +1806,81 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
             NUQ_VD_DMA(0, 0)
 #pragma unroll
             for (uint32_t t = 0; t < 4; ++t) sft[t] = 0.f;
+            const uint32_t ap3 = r16 >> 2, at3 = r16 & 3;
 #pragma unroll
-            for (uint32_t t = 0; t < 3; ++t) {
-                if (t >= tokens) continue;
-                const float f[8] = {fl[t][0].x, fl[t][0].y, fl[t][0].z, fl[t][0].w,
-                                    fl[t][1].x, fl[t][1].y, fl[t][1].z, fl[t][1].w};
-                float amax = 0.f, cs = 0.f;
+            for (uint32_t ph = 0; ph < 2; ++ph) {
+                if (2 * ph >= tokens) break;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    amax = fmaxf(amax, fabsf(f[k]));
-                    cs += f[k];
-                }
-                if (!live_k) amax = cs = 0.f;
-                amax = vd_wave_max(amax);
-                // group sums: the four lanes of a 32-value group
-                cs += vd_dpp<0xb1>(cs);
-                cs += vd_dpp<0x4e>(cs);
-                // lane (r16, h) of part 0 of this token keeps the sums of
-                // groups 2h, 2h + 1 of each block: lanes 32s + 8h + 4q
+                for (uint32_t tt = 0; tt < 2; ++tt) {
+                    const uint32_t t = 2 * ph + tt;
+                    if (t >= tokens) continue;
+                    const float f[8] = {fl[t][0].x, fl[t][0].y, fl[t][0].z, fl[t][0].w,
+                                        fl[t][1].x, fl[t][1].y, fl[t][1].z, fl[t][1].w};
+                    float amax = 0.f, cs = 0.f;
 #pragma unroll
-                for (uint32_t sb = 0; sb < 2; ++sb)
-#pragma unroll
-                    for (uint32_t q = 0; q < 2; ++q) {
-                        const float g = __shfl(cs, 32 * sb + 8 * h + 4 * q, 64);
-                        if ((r16 & 3) == t) gs3[sb][q] = g;
+                    for (int k = 0; k < 8; ++k) {
+                        amax = fmaxf(amax, fabsf(f[k]));
+                        cs += f[k];
                     }
-                // 2^e with the run's largest |x| * 2^e in [2^14, 2^15); 1 for
-                // zero or non-finite runs (non-finite values reach the MFMA)
-                int ex = 0;
-                if (amax > 0.f && amax <= 3.0e38f) {
-                    (void)frexpf(amax, &ex);
-                    ex = 15 - ex;
-                }
-                sft[t] = ldexpf(1.f, -ex);
-                half8 p0, p1, p2;
+                    if (!live_k) amax = cs = 0.f;
+                    amax = vd_wave_max(amax);
+                    // group sums: the four lanes of a 32-value group
+                    cs += vd_dpp<0xb1>(cs);
+                    cs += vd_dpp<0x4e>(cs);
+                    // lane (r16, h) of part 0 of this token keeps the sums of
+                    // groups 2h, 2h + 1 of each block: lanes 32s + 8h + 4q
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float xv = ldexpf(f[k], ex);
-                    p0[k] = (_Float16)xv;
-                    const float r1 = xv - (float)p0[k];
-                    p1[k] = (_Float16)r1;
-                    p2[k] = (_Float16)(r1 - (float)p1[k]);
+                    for (uint32_t sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (uint32_t q = 0; q < 2; ++q) {
+                            const float g = __shfl(cs, 32 * sb + 8 * h + 4 * q, 64);
+                            if (at3 == t) gs3[sb][q] = g;
+                        }
+                    // 2^e with the run's largest |x| * 2^e in [2^14, 2^15); 1 for
+                    // zero or non-finite runs (non-finite values reach the MFMA)
+                    int ex = 0;
+                    if (amax > 0.f && amax <= 3.0e38f) {
+                        (void)frexpf(amax, &ex);
+                        ex = 15 - ex;
+                    }
+                    sft[t] = ldexpf(1.f, -ex);
+                    half8 p0, p1, p2;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const float xv = ldexpf(f[k], ex);
+                        p0[k] = (_Float16)xv;
+                        const float r1 = xv - (float)p0[k];
+                        p1[k] = (_Float16)r1;
+                        p2[k] = (_Float16)(r1 - (float)p1[k]);
+                    }
+                    if (live_k) {
+                        uint32_t dst = vd_lds_addr(xs + tt * span + 16 * lane);
+                        const uint32_t pst = 2 * span;
+                        asm volatile("ds_write_b128 %0, %1\n\t"
+                                     "v_add_u32 %0, %0, %4\n\t"
+                                     "ds_write_b128 %0, %2\n\t"
+                                     "v_add_u32 %0, %0, %4\n\t"
+                                     "ds_write_b128 %0, %3"
+                                     : "+&v"(dst)
+                                     : "v"(__builtin_bit_cast(u32x4, p0)), "v"(__builtin_bit_cast(u32x4, p1)),
+                                       "v"(__builtin_bit_cast(u32x4, p2)), "v"(pst)
+                                     : "memory");
+                    }
                 }
-                if (live_k) {
-                    uint32_t dst = vd_lds_addr(xs + t * span + 16 * lane);
-                    const uint32_t pst = tokens * span;
-                    asm volatile("ds_write_b128 %0, %1\n\t"
-                                 "v_add_u32 %0, %0, %4\n\t"
-                                 "ds_write_b128 %0, %2\n\t"
-                                 "v_add_u32 %0, %0, %4\n\t"
-                                 "ds_write_b128 %0, %3"
-                                 : "+&v"(dst)
-                                 : "v"(__builtin_bit_cast(u32x4, p0)), "v"(__builtin_bit_cast(u32x4, p1)),
-                                   "v"(__builtin_bit_cast(u32x4, p2)), "v"(pst)
-                                 : "memory");
+                // this phase's part rows are written (one wave: its LDS
+                // accesses complete in order); its lanes read their fragments
+                asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+                if (ap3 < 3 && at3 < tokens && (at3 >> 1) == ph) {
+                    const uint32_t xa = vd_lds_addr(xs) + (2 * ap3 + (at3 & 1)) * span + 128 * h;
+                    vd_read_x<0>(xa, xr3[0]);
+                    if (nlive > 1) vd_read_x<512>(xa, xr3[1]);
+                    // the reads land before the next phase writes over the
+                    // rows, and before anything reads the registers
+                    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+#pragma unroll
+                    for (uint32_t s = 0; s < NB; ++s)
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) asm volatile("" : "+v"(xr3[s][c]));
                 }
             }
         } else {
@@ -1878,9 +1903,13 @@ __global__ void __launch_bounds__(64 * vd_max_waves<NB>()) verify_dma_kernel(con
         const uint32_t ap = r16 >> 2, at = r16 & 3;
         const bool arow = XS == 3 ? ap < 3 && at < tokens : r16 < tokens;
         u32x4 xr[NB][8] = {};  // a wave's block past the row's end stays zero
-        {
-            // XS = 3: staging row pT + t
-            const uint32_t srow = XS == 3 ? (arow ? ap * tokens + at : 0) : (arow ? r16 : 0);
+        if constexpr (XS == 3) {
+#pragma unroll
+            for (uint32_t s = 0; s < NB; ++s)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) xr[s][c] = xr3[s][c];
+        } else {
+            const uint32_t srow = arow ? r16 : 0;
             const uint32_t xa = vd_lds_addr(xs) + srow * span + 128 * h;
             vd_read_x<0>(xa, xr[0]);
             if (nlive > 1) vd_read_x<512>(xa, xr[1]);
@@ -2108,14 +2137,14 @@ __global__ void verify_reduce_kernel(const float *__restrict__ ws, uint32_t nran
 // Streams when the row's blocks fit 12 waves of at most 2 blocks, or, with a
 // workspace, in K ranges of at most 24 blocks whose sums verify_reduce_kernel
 // adds; returns false (nothing launched) otherwise.
-// xs3: F32 activations of at most 5 tokens as three f16 parts each (the
+// xs3: F32 activations of at most 4 tokens as three f16 parts each (the
 // kernel's XS = 3): F32 precision.
 template <uint32_t ENC>
 static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t nblocks_all,
                               const void *x, uint32_t x_f16, uint64_t in_stride, float *y_out,
                               uint64_t out_stride_out, uint32_t out_tokens, hipError_t *err,
                               const SplitScratch *scratch = nullptr, bool xs3 = false) {
-    if (xs3 && (x_f16 || out_tokens > 3)) return false;
+    if (xs3 && (x_f16 || out_tokens > 4)) return false;
     const uint32_t tokens = out_tokens;
     constexpr uint32_t MAXW = vd_max_waves<2>();
     constexpr size_t LDS = 160 * 1024;
@@ -2184,8 +2213,8 @@ static bool launch_verify_dma(hipStream_t s, const uint8_t *w, uint64_t stride, 
     uint32_t max_run = 0;
     for (uint32_t k = 0; k < waves; ++k) max_run = std::max(max_run, (k + 1) * nblocks / waves - k * nblocks / waves);
     // staged activations per wave: f16 rows, or (xs3) three part rows per
-    // token
-    const size_t xwave = (size_t)(xs3 ? 3 : 1) * tokens * max_run * 512;
+    // token of a staging phase (two tokens)
+    const size_t xwave = (size_t)(xs3 ? 3 * std::min(tokens, 2u) : tokens) * max_run * 512;
     const size_t xall = (size_t)tokens * nblocks * 512;
     const size_t per_row = (size_t)waves * tpad * 4;
     // One workgroup per CU when the partial sums of its rows fit, else more,
@@ -2330,7 +2359,7 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                             uint32_t columns, const float *x, uint64_t in_stride, float *y, uint64_t out_stride,
                             uint32_t tokens, const SplitScratch &scratch) {
-    if (tokens < 1 || tokens > 3 || columns % 256 != 0) return hipErrorInvalidValue;
+    if (tokens < 1 || tokens > 4 || columns % 256 != 0) return hipErrorInvalidValue;
     hipError_t err = hipErrorInvalidValue;
     bool launched = false;
     if (encoding == 12)

@@ -77,7 +77,7 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);
 uint32_t split_scratch_tiles();
-// Multi-token GEMV of F32 activations (1..3 tokens) at F32 precision on the
+// Multi-token GEMV of F32 activations (1..4 tokens) at F32 precision on the
 // matrix cores (the streamed verify tile with each token's activations as
 // three f16 parts); Q4_K / Q5_K. hipErrorInvalidValue (nothing launched)
 // for shapes it does not take.

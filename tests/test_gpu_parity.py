@@ -643,6 +643,31 @@ def test_multi_token_f32_matches_oracle(backend, encoding, rows, columns, tokens
     assert np.array_equal(got.view(np.uint32), out2.cpu().numpy()[:, :rows].view(np.uint32))
 
 
+# Four F32 token rows in one launch of the multi-token MFMA form (matvecRows;
+# the parts go through the staging two tokens at a time): the plain F32 bound,
+# with one token spread over twelve binary decades inside each run.
+@pytest.mark.parametrize("encoding,rows,columns", sorted({(e, r, c) for (e, r, c, _) in MULTI_TOKEN_CASES}))
+def test_matvec_rows_four_tokens_f32(backend, encoding, rows, columns):
+    import torch
+    tokens = 4
+    w = quantized(encoding, rows, columns, 99)
+    rng = np.random.default_rng(98)
+    x = gaussian(100, (tokens, columns))
+    x[2] *= np.exp2(rng.uniform(-6, 6, columns)).astype(np.float32)
+    in_stride, out_stride = columns + 4, rows + 8
+    xs = np.zeros((tokens, in_stride), np.float32)
+    xs[:, :columns] = x
+    print(f"[rows-4] enc {encoding} {rows}x{columns}", flush=True)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    out = torch.full((tokens, out_stride), np.nan, device="cuda")
+    backend.matvec_rows(m, to_gpu(xs), in_stride, out, out_stride, tokens)
+    backend.sync()
+    want = orc.matmul(encoding, rows, columns, w, x)
+    got = out.cpu().numpy()
+    check_close(got[:, :rows], want, mass(encoding, w, rows, columns, x), F32_K, f"rows-4 {encoding}")
+    assert np.isnan(got[:, rows:]).all()
+
+
 # Graph replays of the streamed kernels: the matmul routes (decode GEMV,
 # F32 multi-token, verify tile with register-staged or ringed steps, K ranges
 # with their reduce, prefill) captured in a HIP graph, replayed with eager
@@ -685,7 +710,7 @@ def test_matmul_graph_replays_match_eager(backend, encoding, rows, columns, toke
 
 
 # matvecRows with 4..8 F32 token rows (Q4_K / Q5_K) runs as launches of the
-# F32 multi-token MFMA form over 3 and 2 tokens: within the plain F32 bound,
+# F32 multi-token MFMA form over at most 4 tokens: within the plain F32 bound,
 # and each chunk's tokens bit-identical to the same tokens served alone.
 @pytest.mark.parametrize("encoding,rows,columns", [(12, 4104, 5120), (13, 1040, 5120), (12, 1040, 17408)])
 @pytest.mark.parametrize("tokens", [4, 5, 8])
@@ -700,7 +725,7 @@ def test_matvec_rows_in_chunks_matches_oracle(backend, encoding, rows, columns, 
     backend.matvec_rows(m, xg, columns, out, rows, tokens)
     out2 = torch.full((tokens, rows), np.nan, device="cuda")
     backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, out2, rows, tokens)
-    first = 2 if tokens == 4 else 3
+    first = 3 if tokens == 4 else 4  # (4 tokens: the first three alone)
     alone = torch.full((first, rows), np.nan, device="cuda")
     backend.matvec_rows(m, xg[:first].contiguous(), columns, alone, rows, first)
     backend.sync()
