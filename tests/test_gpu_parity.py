@@ -668,6 +668,26 @@ def test_matvec_rows_four_tokens_f32(backend, encoding, rows, columns):
     assert np.isnan(got[:, rows:]).all()
 
 
+# A NaN in one token's activations: that token's rows are all NaN, as the
+# oracle's F64 sums are, and the other tokens of the same launch are unaffected.
+@pytest.mark.parametrize("tokens", [2, 4])
+def test_matvec_rows_nan_token_stays_in_its_rows(backend, tokens):
+    import torch
+    encoding, rows, columns = 12, 1040, 5120
+    w = quantized(encoding, rows, columns, 101)
+    x = gaussian(102, (tokens, columns))
+    x[tokens - 1, 777] = np.nan
+    print(f"[rows-nan] T={tokens}", flush=True)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    out = torch.zeros((tokens, rows), device="cuda")
+    backend.matvec_rows(m, to_gpu(x), columns, out, rows, tokens)
+    backend.sync()
+    got = out.cpu().numpy()
+    assert np.isnan(got[tokens - 1]).all()
+    want = orc.matmul(encoding, rows, columns, w, x[:tokens - 1])
+    check_close(got[:tokens - 1], want, mass(encoding, w, rows, columns, x[:tokens - 1]), F32_K, "rows-nan")
+
+
 # Graph replays of the streamed kernels: the matmul routes (decode GEMV,
 # F32 multi-token, verify tile with register-staged or ringed steps, K ranges
 # with their reduce, prefill) captured in a HIP graph, replayed with eager
