@@ -2373,8 +2373,26 @@ hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, 
 
 uint32_t split_scratch_tiles() { return 4 * compute_units(); }
 
+// Q4_K / Q5_K with up to VF_PASS_MAX tokens (K a multiple of 256) run on the
+// streamed verify tile in passes of at most 16 tokens, each pass reading the
+// weights once; more tokens, and the other encodings past 16 tokens, go to
+// the prefill tile. 17408 x 5120 Q4_K: 17 / 24 / 32 / 48 tokens 0.033 /
+// 0.034 / 0.047 / 0.070 ms in passes against 0.075-0.078 on the prefill
+// tile (and 0.108-0.126 on the 128 x 128 tile); Q6_K 5120 x 17408, whose
+// verify tile is the register form, 0.083 in passes at 17 tokens against
+// 0.078.
+constexpr uint32_t VF_PASS_MAX = 48;
+static bool vf_passes(uint32_t encoding, uint32_t tokens, uint32_t columns) {
+    return (encoding == 12 || encoding == 13) && tokens > 16 && tokens <= VF_PASS_MAX && columns % 256 == 0;
+}
+static uint32_t vf_pass_tokens(uint32_t tokens) {
+    const uint32_t passes = (tokens + 15) / 16;
+    return (tokens + passes - 1) / passes;
+}
+
 uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t columns, uint32_t tokens,
                                uint64_t in_stride, bool xs3) {
+    if (vf_passes(encoding, tokens, columns)) tokens = vf_pass_tokens(tokens);
     if (tokens <= 16 && columns % 256 == 0) {
         // the streamed verify tile's K ranges (Q4_K / Q5_K rows longer than
         // 2 * MAXW blocks, or 20 for the F32 multi-token form), one F32
@@ -2384,7 +2402,7 @@ uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t column
         if ((encoding != 12 && encoding != 13) || nblocks <= max_kb || rows < 16) return 0;
         return (uint64_t)((nblocks + max_kb - 1) / max_kb) * tokens * rows;
     }
-    if (tokens > 128 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {  // as launch_tile routes
+    if (tokens > 16 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {  // as launch_tile routes
         const uint32_t cus = compute_units();
         const uint32_t tiles = ((tokens + PF_BM - 1) / PF_BM) * ((rows + PF_BN - 1) / PF_BN);
         uint32_t full, tail, splits;
@@ -2397,6 +2415,18 @@ uint64_t tile_workspace_floats(uint32_t encoding, uint32_t rows, uint32_t column
 hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch) {
+    if (vf_passes(encoding, tokens, columns)) {
+        const uint32_t chunk = vf_pass_tokens(tokens);
+        const size_t xe = x_f16 ? 2 : 4;
+        for (uint32_t t0 = 0; t0 < tokens; t0 += chunk) {
+            const hipError_t e = launch_tile(s, encoding, w, stride, rows, columns,
+                                             (const uint8_t *)x + (uint64_t)t0 * in_stride * xe, x_f16, in_stride,
+                                             y + (uint64_t)t0 * out_stride, out_stride, std::min(chunk, tokens - t0),
+                                             scratch);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     if (tokens <= 16 && columns % 256 == 0) {
         switch (encoding) {
         case 12: return launch_verify_enc<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch);
@@ -2407,7 +2437,7 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
         }
     }
     // (the prefill tile's activation copies use 32-bit offsets within a tile)
-    if (tokens > 128 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {
+    if (tokens > 16 && (uint64_t)PF_BM * in_stride * 2 + 256 <= 0xffffffffull) {
         const uint32_t cus = compute_units();
         switch (encoding) {
         case 12: return launch_prefill<12>(s, w, stride, rows, columns, x, x_f16, in_stride, y, out_stride, tokens, scratch, cus);

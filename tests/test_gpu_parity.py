@@ -245,6 +245,12 @@ TILE_CASES = [
     # Q5_K and IQ4_XS at verify, tile and prefill token counts
     (13, 512, 5120, 8), (23, 512, 5120, 8), (13, 256, 1280, 37), (23, 256, 1280, 37),
     (13, 520, 2048, 300), (23, 520, 2048, 300),
+    # Q4_K / Q5_K at 17-48 tokens: verify passes of at most 16 tokens (ragged
+    # last pass; K ranges and their workspace per pass), then the prefill tile
+    (12, 1040, 5120, 33), (13, 1040, 17408, 48), (12, 1040, 5120, 49),
+    # K not a multiple of 256 (Q8_0): the 128 x 128 tile, and the prefill
+    # tile without a K split
+    (8, 264, 4160, 8), (8, 264, 4160, 40),
 ]
 
 
