@@ -8,8 +8,10 @@ A "step" is one Q4_K GEMV over one weight copy: y = W x, W 17408 x 5120 Q4_K
 one replay of a HIP graph of exactly --steps back-to-back GEMVs that rotate
 over enough distinct weight copies (>= 512 MB) that every call streams from
 HBM and not from the 256 MB Infinity Cache, after --warmup launches of the
-same rotation. `value` = weight bytes x steps / the region's duration, from
-HIP events on the launch stream; the roofline uses the algorithmic bytes
+same rotation and a lead of at least 100 more: the lead still runs while the
+region's start event and graph are queued behind it, so the region holds no
+host submission latency. `value` = weight bytes x steps / the region's
+duration, from HIP events on the launch stream; the roofline uses the algorithmic bytes
 (weights + x + y) per launch over the same average launch duration.
 
 Every other configuration runs by default with its own fixed repetition
@@ -43,8 +45,9 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
 MALL_BYTES = 256 << 20
 GEMV_KERNEL = "gemv_dma_kernel<12, 4, 2, false, false>"
-GEMV_DTYPE = ("q4_k codes x f32 activations carried as 24-bit fixed point per 32-value slice "
-              "(three int8 byte planes, exact int32 dot; F32-mantissa precision) -> f32 scale/accumulate")
+GEMV_DTYPE = ("q4_k codes x f32 activations as fixed point relative to each 32-value slice's maximum "
+              "(power-of-two slice scale, 23 significant bits, three int8 byte planes into an exact int32 dot) "
+              "-> f32 scale/accumulate")
 
 
 def parse():
@@ -56,7 +59,8 @@ def parse():
                    help="also time the lm_head GEMV, Q5_K / IQ4_XS, GGUF upload and sampling")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", default="", help="comma list of: configs, prefill (the headline GEMV always runs)")
+    p.add_argument("--only", default="",
+                   help="comma list of: configs, prefill, gemv (the headline GEMV always runs; gemv alone runs only it)")
     p.add_argument("--case", default="",
                    help="profiling aid: only time one matmul, ENC:ROWS:COLUMNS:TOKENS (f16 activations), e.g. 14:5120:17408:4096")
     p.add_argument("--profile-copy", action="store_true",
@@ -192,14 +196,17 @@ def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmu
         timed = capture(steps)
         # The GPU's clocks settle over the first few hundred microseconds of
         # load: at least 200 launches in all replay untimed before the timed
-        # region (the `warmup` requested, plus a pre-warm reported apart).
-        prewarm = max(0, 200 - warmup)
+        # region (the `warmup` requested, plus a lead reported apart). The
+        # lead's replay is not waited for: the start event and the timed
+        # graph are queued behind it while it runs, so the region starts on
+        # a busy GPU and holds no host submission latency.
+        lead = max(100, 200 - warmup)
         if warmup:
             capture(warmup).replay()
-        if prewarm:
-            capture(prewarm).replay()
+        lead_graph = capture(lead)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        lead_graph.replay()
         with Timer(torch, stream) as t:
             timed.replay()
         torch.cuda.synchronize()
@@ -210,12 +217,12 @@ def bench_gemv(torch, nq, backend, stream, encoding, rows, columns, steps, warmu
     algo_bytes = weight_bytes + columns * 4 + rows * 4
     kernel_s = t.ms / 1e3 / steps
     return {
-        "launches": steps, "warmup_launches": warmup, "prewarm_launches": prewarm, "copies": ncopies, "wall_s": wall, "event_ms": t.ms,
+        "launches": steps, "warmup_launches": warmup, "lead_launches": lead, "copies": ncopies, "wall_s": wall, "event_ms": t.ms,
         "weight_bytes": weight_bytes, "algo_bytes": algo_bytes,
         "us_per_launch": kernel_s * 1e6,
         "weight_gbs": weight_bytes / kernel_s / 1e9,
         "algo_gbs": algo_bytes / kernel_s / 1e9,
-        "wall_weight_gbs": weight_bytes * steps / wall / 1e9,
+        "wall_weight_gbs": weight_bytes * (steps + lead) / wall / 1e9,  # host clock over lead + region
         "w": w, "x": x, "y0": eager[0],
     }
 
@@ -267,9 +274,11 @@ def bench_gemm(torch, nq, backend, stream, encoding, rows, columns, tokens, reps
 
     stream.wait_stream(torch.cuda.current_stream())  # inputs were made on the default stream
     with torch.cuda.stream(stream):
+        call(mats[0])
+        torch.cuda.synchronize()
+        # the warm-up launches are not waited for: the timed ones queue behind them
         for i in range(warmup):
             call(mats[i % len(mats)])
-        torch.cuda.synchronize()
         with Timer(torch, stream) as t:
             for i in range(reps):
                 call(mats[i % len(mats)])
@@ -341,6 +350,8 @@ def bench_layer(torch, nq, backend, stream, reps=20, check=None):
             graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(dev.buffers["logits"], eager), "graph replay differs from the eager step"
+        for _ in range(5):  # lead replays, not waited for: the timed ones queue behind them
+            graph.replay()
         with Timer(torch, stream) as t:
             for _ in range(reps):
                 graph.replay()
@@ -511,7 +522,7 @@ def main():
                                f"{g['copies']} rotating weight copies; value = weight bytes x steps / "
                                "event-timed region (one graph replay of exactly `steps` launches)",
                    "weight_bytes": g["weight_bytes"], "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
-                   "prewarm_launches": g["prewarm_launches"],
+                   "lead_launches": g["lead_launches"],
                    "wall_weight_gbs": round(g["wall_weight_gbs"], 2), "parity": gcheck},
         "roofline": {"bound": "hbm", "achieved": round(g["algo_bytes"] / kernel_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["algo_bytes"] / kernel_s / 1e9 / HBM_PEAK_GBS, 4),

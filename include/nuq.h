@@ -88,14 +88,18 @@ void nuq_destroy(nuq_context *ctx);
 /* Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
  * When the stream changes, the new stream first waits for the work already
  * enqueued on the old one (the context's workspace is shared by its calls),
- * unless either stream is capturing a graph. */
+ * unless either stream is capturing a graph. The previous stream must still
+ * be alive when this is called (an event is recorded on it). */
 int nuq_set_stream(nuq_context *ctx, void *stream);
 /* The context's device workspace (verify K-range partials, prefill split
  * partials, the SiLU pair's second GEMV) is allocated on the first call that
  * wants it and grown as needed; nuq_create allocates none. A call that would
- * grow it while its stream captures a graph takes its no-workspace route
- * instead (same products). Callers that capture graphs may reserve it
- * beforehand. No counterpart in the reference (Metal buffers are created per
+ * grow it while a graph capture is active takes its no-workspace route
+ * instead (same products). A workspace that a captured call used is never
+ * freed on growth: it stays allocated until nuq_destroy, so graphs captured
+ * earlier keep replaying into valid memory (they must not replay after
+ * nuq_destroy). Callers that capture graphs may reserve it beforehand, so it
+ * never grows after a capture. No counterpart in the reference (Metal buffers are created per
  * use, backends/metal/root.zig:62-86). */
 int nuq_reserve_workspace(nuq_context *ctx, uint64_t bytes);
 /* Bytes of workspace the context currently holds. */

@@ -39,6 +39,10 @@ struct nuq_context {
     // the SiLU pair's second GEMV: allocated on the first call that wants it
     // and grown in whole 256 x 256 tiles (ensure_workspace)
     nuq::SplitScratch split{nullptr, 0};
+    // The current workspace was handed to a launch recorded into a graph:
+    // on growth it is kept (the graph may replay) rather than freed.
+    bool split_captured = false;
+    std::vector<float *> retired;  // such earlier workspaces, freed by nuq_destroy
     uint64_t *topk_keys = nullptr;  // partial top-k keys between passes
     hipEvent_t handoff = nullptr;   // orders work across a stream change
     float *static_scratch = nullptr;  // this device's copy of `scratch` (below)
@@ -72,31 +76,59 @@ int hip_check(nuq_context *ctx, hipError_t e, const char *what) {
     return fail(ctx, NUQ_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Whether work enqueued now on `stream` would be recorded into a graph, or
+// a device-wide call now could disturb a capture: the context's stream is
+// capturing, or a query fails (the legacy stream reports an implicit
+// capture error while another stream captures in global mode).
+bool capture_active(hipStream_t stream) {
+    hipStreamCaptureStatus a = hipStreamCaptureStatusNone, b = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &a) != hipSuccess || a != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return true;
+    }
+    if (stream != nullptr && (hipStreamIsCapturing(nullptr, &b) != hipSuccess || b != hipStreamCaptureStatusNone)) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return false;
+}
+
 // Grows the context workspace to at least `floats` F32 values (whole 256 x
 // 256 tiles). Returns false, leaving it as it was, when the allocation fails
-// or the context's stream is capturing a graph (an allocation cannot be
-// captured): the caller's route then takes its no-workspace form, which
-// computes the same products. Growing waits for the device, since work in
-// flight may still use the old buffer.
+// or a graph capture is active (an allocation cannot be captured): the
+// caller's route then takes its no-workspace form, or fewer splits of the
+// workspace it has, which compute the same products. A call made while its
+// stream captures marks the current workspace as captured; growing later
+// then keeps that buffer alive until nuq_destroy (a graph replay writes to
+// it), and otherwise frees it once the context's stream has finished with
+// it (a stream change orders the new stream after the old, so that wait
+// covers every call of the context).
 bool ensure_workspace(nuq_context *ctx, uint64_t floats) {
     constexpr uint64_t TILE = 256 * 256;
     if (floats == 0) return true;
     const uint64_t tiles = (floats + TILE - 1) / TILE;
+    if (capture_active(ctx->stream)) {
+        if (ctx->split.work) ctx->split_captured = true;
+        return tiles <= ctx->split.tiles;
+    }
     if (tiles <= ctx->split.tiles) return true;
     if (tiles > 0xffffffffull) return false;
-    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return false;
     float *p = nullptr;
     if (hipMalloc((void **)&p, tiles * TILE * sizeof(float)) != hipSuccess) {
         (void)hipGetLastError();
         return false;
     }
     if (ctx->split.work) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->split.work);
+        if (ctx->split_captured) {
+            ctx->retired.push_back(ctx->split.work);
+        } else {
+            (void)hipStreamSynchronize(ctx->stream);
+            (void)hipFree(ctx->split.work);
+        }
     }
     ctx->split.work = p;
     ctx->split.tiles = (uint32_t)tiles;
+    ctx->split_captured = false;
     return true;
 }
 
@@ -201,12 +233,14 @@ int run_rows_mfma(nuq_context *ctx, const nuq_matrix *m, uint64_t stride, const 
                                                            std::min(tokens, 4u), in_stride, true));
     for (uint32_t t0 = 0; t0 < tokens;) {
         const uint32_t c = std::min(tokens - t0, 4u);
+        bool taken = false;
         const hipError_t e = nuq::launch_rows_mfma(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,
                                                    (uint32_t)m->rows, (uint32_t)m->columns, x + t0 * in_stride,
-                                                   in_stride, out + t0 * out_stride, out_stride, c, ctx->split);
+                                                   in_stride, out + t0 * out_stride, out_stride, c, ctx->split, &taken);
         // a shape the form does not take is refused by the first launch,
         // before anything runs (later launches have the same or fewer tokens)
-        if (e == hipErrorInvalidValue && t0 == 0) return -1;
+        if (!taken && t0 == 0) return -1;
+        if (!taken) return fail(ctx, NUQ_DEVICE_ERROR, "multi-token gemv: a later pass of %u tokens was refused", c);
         const int r = hip_check(ctx, e, "multi-token gemv launch");
         if (r) return r;
         t0 += c;
@@ -334,7 +368,9 @@ void nuq_destroy(nuq_context *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->argmax_buf) (void)hipFree(ctx->argmax_buf);
+    (void)hipStreamSynchronize(ctx->stream);
     if (ctx->split.work) (void)hipFree(ctx->split.work);
+    for (float *p : ctx->retired) (void)hipFree(p);
     if (ctx->topk_keys) (void)hipFree(ctx->topk_keys);
     if (ctx->handoff) (void)hipEventDestroy(ctx->handoff);
     delete ctx;

@@ -2358,9 +2358,10 @@ static hipError_t launch_tile_enc(hipStream_t s, const uint8_t *w, uint64_t stri
 
 hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                             uint32_t columns, const float *x, uint64_t in_stride, float *y, uint64_t out_stride,
-                            uint32_t tokens, const SplitScratch &scratch) {
-    if (tokens < 1 || tokens > 4 || columns % 256 != 0) return hipErrorInvalidValue;
-    hipError_t err = hipErrorInvalidValue;
+                            uint32_t tokens, const SplitScratch &scratch, bool *taken) {
+    *taken = false;
+    if (tokens < 1 || tokens > 4 || columns % 256 != 0) return hipSuccess;
+    hipError_t err = hipSuccess;
     bool launched = false;
     if (encoding == 12)
         launched = launch_verify_dma<12>(s, w, stride, rows, columns / 256, x, 0, in_stride, y, out_stride, tokens,
@@ -2368,7 +2369,8 @@ hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, 
     else if (encoding == 13)
         launched = launch_verify_dma<13>(s, w, stride, rows, columns / 256, x, 0, in_stride, y, out_stride, tokens,
                                          &err, &scratch, true);
-    return launched ? err : hipErrorInvalidValue;
+    *taken = launched;
+    return launched ? err : hipSuccess;
 }
 
 uint32_t split_scratch_tiles() { return 4 * compute_units(); }

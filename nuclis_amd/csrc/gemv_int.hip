@@ -7,17 +7,26 @@
 // int32 accumulation.
 //
 // Activations: every lane keeps a fixed slice of x for the whole kernel
-// (the K-split below), so it converts that slice once to 24-bit fixed point,
-// as many significant bits as an F32 mantissa: per 32-value slice, scale
-// s = max|x| / 8355711 and x24 = rint(x / s), split exactly into three
-// signed bytes x24 = 65536*xh + 256*xm + xl (each in [-128, 127]). A code q
-// then contributes q*x24 = 65536*(q*xh) + 256*(q*xm) + q*xl: three dot4
-// accumulations, each exact in int32. The only approximation before the
-// F32 scale and accumulate is x's rounding to 24 bits of its slice maximum
-// (|error| <= max|x| / 16711422 + a rounding of the F32 product, about
-// 1.2e-7 * max|x| per element); the per-group affine terms (scale,
-// minimum) are applied in F32. Non-finite activations make the affected
-// outputs NaN.
+// (the K-split below), so it converts that slice once to fixed point with
+// 23 significant bits (an F32 mantissa has 24): per 32-value slice, a
+// power-of-two scale s = 2^-k is picked so that max|x| / s lies in
+// (4194303, 8355711], and x24 = rint(x / s) (an exact ldexp, then one
+// rounding) is split exactly into three signed bytes x24 = 65536*xh +
+// 256*xm + xl (each in [-128, 127]). A code q then contributes q*x24 =
+// 65536*(q*xh) + 256*(q*xm) + q*xl: three dot4 accumulations, each exact in
+// int32. The only approximation before the F32 scale and accumulate is x's
+// rounding, |error| <= s/2 <= max|x| * 1.2e-7 (2.4e-7 when max|x| sits just
+// above a power of two); the per-group affine terms (scale, minimum) are
+// applied in F32. The scale is a power of two at every finite magnitude, so
+// nothing overflows: slices of any size keep their relative precision down
+// to max|x| = 2^-127, below which s underflows and the slice reads as zero.
+//
+// Non-finite activations take no part in the fixed-point planes (their
+// codes are 0 and they are left out of the slice sum); two 32-bit masks per
+// slice mark +Inf/NaN and -Inf/NaN, and the lanes whose slices hold any add
+// decoded_weight * x for those values in F32, so a row's output is +-Inf or
+// NaN exactly as cpu.matvec's F64 products make it (w * +-Inf = +-Inf,
+// 0 * Inf = NaN, w * NaN = NaN; backends/cpu/root.zig:144-152).
 //
 // Layout (K-split, persistent rows): a workgroup of W waves owns a range of
 // rows; wave w owns the block range [4P*w, 4P*w + 4P) of every row, so its
@@ -46,13 +55,13 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 struct XSlice {
     uint32_t hi[8], mid[8], lo[8];
     float scale;
-    float sum;
-    float poison;  // NaN when the slice holds a non-finite value, else 0
+    float sum;                // F32 sum of the slice's finite values
+    uint32_t pos, neg;        // bit c: x[c] is +Inf or NaN (pos), -Inf or NaN (neg)
     // Q6_K only (registers): 32 * sum(x24) over values 0-15 and 16-31
     float bias[2];
 };
 
-// LDS image of one quantised slice: 24 plane dwords + scale, sum, poison, pad.
+// LDS image of one quantised slice: 24 plane dwords + scale, sum, pos, neg.
 constexpr int SLICE_WORDS = 28;
 constexpr float X24_MAX = 8355711.f;  // 127 * (65536 + 256 + 1): every byte of the split in [-128, 127]
 
@@ -116,23 +125,42 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
         v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
     float amax = 0.f, sum = 0.f;
-    bool finite = true;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        finite = finite && isfinite(v[k]);
         amax = fmaxf(amax, fabsf(v[k]));
         sum += v[k];
     }
-    // the pair's halves: lane ^ 1
+    uint32_t pos = 0, neg = 0;
+    if (!isfinite(sum)) {
+        // rare: a non-finite value (the sum of finite ones cannot reach Inf
+        // unless it overflows, which this path handles the same way): mark
+        // them and leave them out of the slice
+        amax = 0.f;
+        sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const bool fin = isfinite(v[k]);
+            pos |= (uint32_t)(!fin && !(v[k] < 0.f)) << k;  // +Inf, NaN
+            neg |= (uint32_t)(!fin && !(v[k] > 0.f)) << k;  // -Inf, NaN
+            v[k] = fin ? v[k] : 0.f;
+            amax = fmaxf(amax, fabsf(v[k]));
+            sum += v[k];
+        }
+    }
+    // the pair's halves: lane ^ 1 (every lane takes part in each exchange)
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
     const float other_sum = __shfl_xor(sum, 1, 64);
-    // every lane must take part in the exchange: written as `finite && shfl`,
-    // the exchange would run only in finite lanes and read a stale value
-    // from a non-finite partner
-    const int partner_finite = __shfl_xor((int)finite, 1, 64);
-    finite = finite && partner_finite != 0;
-    const float scale = amax / X24_MAX;
-    const float inv = amax > 0.f ? X24_MAX / amax : 0.f;
+    const uint32_t other_pos = (uint32_t)__shfl_xor((int)pos, 1, 64);
+    const uint32_t other_neg = (uint32_t)__shfl_xor((int)neg, 1, 64);
+    const uint32_t sh = 16 * half;
+    const uint32_t pos32 = (pos << sh) | (other_pos << (16 - sh)), neg32 = (neg << sh) | (other_neg << (16 - sh));
+    // scale 2^-k: amax * 2^k = f * 2^(e + k) with f in [0.5, 1) from frexp;
+    // k = 23 - e unless that passes X24_MAX (f > 0.99608), then 22 - e
+    int ex;
+    (void)frexpf(amax, &ex);
+    int kx = 23 - ex;
+    if (ldexpf(amax, kx) > X24_MAX) kx -= 1;
+    const float scale = amax > 0.f ? ldexpf(1.f, -kx) : 0.f;
     uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -140,7 +168,7 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // |q| <= 8355711: q = 65536*hi + 256*mi + lo with every part in [-128, 127]
-            const int q = finite ? min(max((int)rintf(v[4 * k + e] * inv), -8355711), 8355711) : 0;
+            const int q = (int)rintf(ldexpf(v[4 * k + e], kx));
             const int lo = ((q + 128) & 255) - 128;
             const int q1 = (q - lo) >> 8;
             const int mi = ((q1 + 128) & 255) - 128;
@@ -154,14 +182,14 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
         lw[k] = l;
     }
     // words: hi plane 0..7, mid plane 8..15, lo plane 16..23, then scale, sum
-    // (lower half first, as the summation order), poison
-    const uint32_t t0 = __float_as_uint(scale), t1 = __float_as_uint(sum + other_sum),
-                   t2 = finite ? 0u : 0x7fc00000u;
+    // (lower half first, as the summation order), the non-finite masks
+    const uint32_t t0 = __float_as_uint(scale),
+                   t1 = __float_as_uint(half == 0 ? sum + other_sum : other_sum + sum), t2 = pos32, t3 = neg32;
     if constexpr (ASM_LDS) {
         lds_store4(lds + 4 * half, hw[0], hw[1], hw[2], hw[3]);
         lds_store4(lds + 8 + 4 * half, mw[0], mw[1], mw[2], mw[3]);
         lds_store4(lds + 16 + 4 * half, lw[0], lw[1], lw[2], lw[3]);
-        if (half == 0) lds_store4(lds + 24, t0, t1, t2, 0u);
+        if (half == 0) lds_store4(lds + 24, t0, t1, t2, t3);
     } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -173,7 +201,7 @@ __device__ __forceinline__ void quantize_half_slice(const XHalf &xh, uint32_t ha
             lds[24] = t0;
             lds[25] = t1;
             lds[26] = t2;
-            lds[27] = 0u;
+            lds[27] = t3;
         }
     }
 }
@@ -201,7 +229,8 @@ __device__ __forceinline__ void read_slice_asm(const uint32_t *lds, XSlice &s) {
     }
     s.scale = __uint_as_float(p[6].x);
     s.sum = __uint_as_float(p[6].y);
-    s.poison = __uint_as_float(p[6].z);
+    s.pos = p[6].z;
+    s.neg = p[6].w;
 }
 
 __device__ __forceinline__ void read_slice(const uint32_t *lds, XSlice &s) {
@@ -213,7 +242,8 @@ __device__ __forceinline__ void read_slice(const uint32_t *lds, XSlice &s) {
     }
     s.scale = __uint_as_float(lds[24]);
     s.sum = __uint_as_float(lds[25]);
-    s.poison = __uint_as_float(lds[26]);
+    s.pos = lds[26];
+    s.neg = lds[27];
 }
 
 // Q6_K's -32 bias per 16-value half of a slice: 32 * sum(x24), from the
@@ -230,6 +260,33 @@ __device__ __forceinline__ void plane_sums(XSlice &s) {
         }
         s.bias[half] = 32.f * combine3(h, m, l);
     }
+}
+
+// The non-finite activations against one row's decoded weights: the sum of
+// w[c] * x[c] over the columns c that the slice masks mark, in F32.
+// cpu.matvec multiplies each F64 weight by its activation
+// (backends/cpu/root.zig:144-152); with x = +-Inf or NaN the class of each
+// product (w * +-Inf = +-Inf, 0 * Inf = NaN, w * NaN = NaN) and of their sum
+// with the finite rest does not depend on the precision. Taken only when a
+// workgroup's x holds such values; `unit_bytes` is 272 for Q8_0 (eight
+// blocks), else the block size.
+__device__ __noinline__ float nonfinite_row(uint32_t enc, const uint8_t *row, uint32_t unit_bytes,
+                                            const uint32_t *slices, uint32_t nslices) {
+    float t = 0.f;
+    for (uint32_t s = 0; s < nslices; ++s) {
+        const uint32_t pos = slices[s * SLICE_WORDS + 26], neg = slices[s * SLICE_WORDS + 27];
+        uint32_t m = pos | neg;
+        while (m) {
+            const uint32_t c = __builtin_ctz(m);
+            m &= m - 1;
+            const float xv = ((pos & neg) >> c) & 1u ? __builtin_nanf("") : ((pos >> c) & 1u ? INFINITY : -INFINITY);
+            const uint32_t col = 32 * s + c;
+            const float wv = enc == 8 ? decode_q8_0(row + (col / 32) * 34, col % 32)
+                                      : decode_value(enc, row + (col / 256) * unit_bytes, col % 256);
+            t += wv * xv;
+        }
+    }
+    return t;
 }
 
 // Q4_K scales/minima of the pair (2j, 2j+1) as floats (quant/decode.zig:155-158),
@@ -365,9 +422,10 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     if (!live) {
         xa.scale = xb.scale = 0.f;
         xa.sum = xb.sum = 0.f;
-        xa.poison = xb.poison = 0.f;
+        xa.pos = xa.neg = xb.pos = xb.neg = 0u;
     }
-    const float poison = xa.poison + xb.poison;
+    // wave-uniform: does any slice this wave reads hold a non-finite value
+    const bool nonfinite = __ballot((xa.pos | xa.neg | xb.pos | xb.neg) != 0u) != 0;
 
     // Step i lives in register slot i % D; once computed, the slot takes
     // step i + D. The main loop runs while every refill is a real step, so
@@ -376,7 +434,7 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
     {                                                                                                        \
         const uint32_t r0_ = first + (STEP_) * set_stride;                                                   \
         _Pragma("unroll") for (int r = 0; r < R; ++r) {                                                      \
-            float v = poison + q4k_lane(hq[SLOT_][r], aq[SLOT_][r], bq[SLOT_][r], xa, xb, shift, direct);    \
+            float v = q4k_lane(hq[SLOT_][r], aq[SLOT_][r], bq[SLOT_][r], xa, xb, shift, direct);              \
             _Pragma("unroll") for (uint32_t off = 2 * SLOTS; off > 0; off >>= 1) v += __shfl_xor(v, off, 64); \
             const uint32_t row = r0_ + g * R + r;                                                            \
             if ((lane & (4 * SLOTS - 1)) == 0 && row < row_end) partial[(row - row_begin) * set_waves + kw] = v; \
@@ -400,10 +458,12 @@ __global__ void __launch_bounds__(GI_WG_THREADS) gemv_q4k_int_kernel(const uint8
         if (i + D + d < nsteps) NUQ_GI_COMPUTE(d, i + D + d)
 #undef NUQ_GI_COMPUTE
 #undef NUQ_GI_LOAD
-    __syncthreads();
+    // every slice is read by some live lane, so this is "x holds a non-finite value"
+    const bool any_nonfinite = __syncthreads_or(nonfinite);
     for (uint32_t i = threadIdx.x; i < row_end - row_begin; i += blockDim.x) {
         float t = 0.f;
         for (uint32_t k = 0; k < set_waves; ++k) t += partial[i * set_waves + k];
+        if (any_nonfinite) t += nonfinite_row(12, w + (uint64_t)(row_begin + i) * stride, 144, slices, nslices);
         y[row_begin + i] = t;
     }
 }
@@ -666,8 +726,10 @@ struct GdEnc<8> {  // Q8_0: eight 34-byte blocks (256 values) as one unit; lane 
             bm = dot4(qb[k], B.mid[k], bm);
             bl = dot4(qb[k], B.lo[k], bl);
         }
-        const float ta = half_bits(da) * A.scale, tb = half_bits(db) * B.scale;
-        return fmaf(ta, combine3(ah, am, al), tb * combine3(bh, bm, bl));
+        // d * sum first, then the slice scale (a power of two): d * scale
+        // alone could fall below the F32 range for tiny activations
+        const float ta = half_bits(da) * combine3(ah, am, al), tb = half_bits(db) * combine3(bh, bm, bl);
+        return fmaf(ta, A.scale, tb * B.scale);
     }
 };
 
@@ -927,9 +989,10 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     if (!live) {
         xa.scale = xb.scale = 0.f;
         xa.sum = xb.sum = 0.f;
-        xa.poison = xb.poison = 0.f;
+        xa.pos = xa.neg = xb.pos = xb.neg = 0u;
     }
-    const float poison = xa.poison + xb.poison;
+    // wave-uniform: does any slice this wave reads hold a non-finite value
+    const bool nonfinite = __ballot((xa.pos | xa.neg | xb.pos | xb.neg) != 0u) != 0;
     const uint32_t role = g * ROW_CHUNKS * 16 + slot * BYTES;
     const uint32_t spare = rows_per_wg * set_waves + wv;  // one spare partial per wave
 
@@ -944,7 +1007,7 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
         e_.template read<VM_>(NUQ_GD_RING(SLOT_) + role, j);                                                \
         REFILL_                                                                                             \
         /* lanes past the row's last block read arbitrary copied bytes: select zero */                     \
-        const float v = group_sum<4 * SLOTS>(poison + (live ? e_.dot(xa, xb, j, shift, direct) : 0.f));      \
+        const float v = group_sum<4 * SLOTS>(live ? e_.dot(xa, xb, j, shift, direct) : 0.f);                \
         const uint32_t row = first + (STEP_) * set_stride + g;                                              \
         /* every lane of the group holds the sum; rows past the range go to a spare slot */               \
         partial[row < row_end ? (row - row_begin) * set_waves + kw : spare] = v;                            \
@@ -969,10 +1032,15 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     // Copies issued for steps past the range (when nsteps < D) must land
     // before the workgroup ends.
     __builtin_amdgcn_s_waitcnt(0x0f70);
+    // Each wave's spare partial now holds its non-finite flag; every slice is
+    // read by some live lane, so their OR is "x holds a non-finite value".
+    if (lane == 0) partial[spare] = nonfinite ? 1.f : 0.f;
     __syncthreads();
+    const bool any_nonfinite = __ballot(partial[rows_per_wg * set_waves + lane % nwaves] != 0.f) != 0;
     for (uint32_t r = threadIdx.x; r < row_end - row_begin; r += blockDim.x) {
         float t = 0.f;
         for (uint32_t k = 0; k < set_waves; ++k) t += partial[r * set_waves + k];
+        if (any_nonfinite) t += nonfinite_row(ENC, w + (uint64_t)(row_begin + r) * stride, BYTES, slices, nslices);
         y[row_begin + r] = t;
     }
 }

@@ -79,11 +79,11 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
 uint32_t split_scratch_tiles();
 // Multi-token GEMV of F32 activations (1..4 tokens) at F32 precision on the
 // matrix cores (the streamed verify tile with each token's activations as
-// three f16 parts); Q4_K / Q5_K. hipErrorInvalidValue (nothing launched)
-// for shapes it does not take.
+// three f16 parts); Q4_K / Q5_K. *taken is false (and nothing launched)
+// for shapes it does not take; otherwise the launch's own status returns.
 hipError_t launch_rows_mfma(hipStream_t s, uint32_t encoding, const uint8_t *w, uint64_t stride, uint32_t rows,
                             uint32_t columns, const float *x, uint64_t in_stride, float *y, uint64_t out_stride,
-                            uint32_t tokens, const SplitScratch &scratch);
+                            uint32_t tokens, const SplitScratch &scratch, bool *taken);
 // F32 workspace the tile route of this call would use (verify K ranges or
 // prefill split partials); 0 when it needs none. A smaller workspace makes
 // the route fall back (fewer splits, or the register verify tile).

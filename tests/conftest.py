@@ -18,5 +18,5 @@ def pytest_terminal_summary(terminalreporter):
     if not WORST:
         return
     terminalreporter.write_line("worst observed |gpu - oracle| / sum|w*x| per check (bound factor k):")
-    for label, (ratio, k) in sorted(WORST.items()):
-        terminalreporter.write_line(f"  {label:24s} {ratio:.3e}  (k = {k:.0e})")
+    for (family, _), (ratio, k, label) in sorted(WORST.items()):
+        terminalreporter.write_line(f"  {family:12s} {ratio:.3e}  (k = {k:.0e})  worst: {label}")

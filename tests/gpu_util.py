@@ -7,17 +7,20 @@ Tolerances (stated where they are used):
     for its matvecs (metal-check.zig:3976), and normwise
     max|gpu - ref| / max|ref| <= 2e-3 (the stated max relative error);
   * the integer-dot decode GEMV holds the same F32 bound: it carries x as
-    24-bit fixed point per 32-value slice (as many bits as an F32
-    mantissa) into an exact integer dot, with no extra term;
+    fixed point with 23 significant bits relative to each 32-value slice's
+    maximum (power-of-two slice scale) into an exact integer dot, with no
+    extra term;
   * f16 MFMA tiles (verify, 128x128 and prefill): weights (and F32
     activations) are rounded to f16, so each term carries at most 2^-11
     relative error per rounded operand; the bound is the reference's own for
     its half tiles, |gpu - ref| <= 2e-4 * sum|w*x| + 1e-6 per output
     (metal-check.zig:3779, 3826, 4424), plus the same 2e-3 normwise bound.
 
-check_close records the worst observed |gpu - ref| / sum|w*x| per label;
-conftest prints the table at the end of the session, so the margin under
-each bound is visible in the test log.
+check_close records the worst observed |gpu - ref| / sum|w*x| per label
+family and bound, with the full label (encoding, shape, tokens) of the case
+that set it; conftest prints the table at the end of the session, so the
+margin under each bound, and where it is smallest, is visible in the test
+log.
 """
 import numpy as np
 
@@ -41,7 +44,7 @@ def mass(encoding, w_bytes, rows, columns, x):
 F32_K = 4e-6   # F32 arithmetic (metal-check.zig:3976)
 F16_K = 2e-4   # half tiles (metal-check.zig:4424)
 
-WORST = {}   # label -> (worst |d| / mass, bound factor k)
+WORST = {}   # (first word of the label, k) -> (worst |d| / mass, k, full label of that case)
 
 
 def check_close(got, want, mass_, k, label="", extra=0.0):
@@ -56,9 +59,9 @@ def check_close(got, want, mass_, k, label="", extra=0.0):
                                   f"(got {got[worst]}, want {want[worst]})")
     m = np.asarray(mass_, np.float64)
     ratio = float(np.max(np.where(m > 0, err / np.where(m > 0, m, 1.0), 0.0))) if err.size else 0.0
-    key = label.split(" ")[0] if label else "unlabelled"
-    if ratio >= WORST.get(key, (-1.0, k))[0]:
-        WORST[key] = (ratio, k)
+    key = (label.split(" ")[0] if label else "unlabelled", k)
+    if ratio >= WORST.get(key, (-1.0, k, ""))[0]:
+        WORST[key] = (ratio, k, label)
     normwise = err.max() / max(np.abs(want).max(), 1e-30)
     assert normwise <= 2e-3, f"{label}: normwise {normwise:.3e}"
     return normwise

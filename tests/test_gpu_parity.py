@@ -555,6 +555,51 @@ def test_workspace_is_allocated_lazily():
         b.close()
 
 
+def test_captured_workspace_survives_growth():
+    """A graph captured with the context's workspace (the verify tile's K
+    ranges) still replays correctly after a later eager call has grown the
+    workspace: the captured buffer is kept until the context is destroyed,
+    not freed on growth, so its memory cannot be handed to a new allocation
+    (filled with garbage here) while the graph still writes to it."""
+    import torch
+    b = nq.Backend(0)
+    try:
+        tokens, rows, columns = 8, 1024, 17408
+        md = nq.Matrix(12, rows, columns, to_gpu(quantized(12, rows, columns, 140)))
+        x = to_gpu(gaussian(141, (tokens, columns)).astype(np.float16))
+        eager = torch.empty((tokens, rows), device="cuda")
+        b.matmul(md, x, columns, eager, rows, tokens)
+        b.sync()
+        small = b.workspace_bytes()
+        assert 0 < small <= 4 << 20
+        out = torch.full((tokens, rows), np.nan, device="cuda")
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                b.matmul(md, x, columns, out, rows, tokens)
+        torch.cuda.synchronize()
+        # an eager prefill that splits K grows the workspace past the captured one
+        pm = nq.Matrix(12, 17408, 5120, to_gpu(quantized(12, 17408, 5120, 142)))
+        xp = to_gpu(gaussian(143, (4096, 5120)).astype(np.float16))
+        yp = torch.empty((4096, 17408), device="cuda")
+        b.matmul(pm, xp, 5120, yp, 17408, 4096)
+        b.sync()
+        assert b.workspace_bytes() > small
+        junk = [torch.full((small // 4,), 7.0, device="cuda") for _ in range(4)]
+        for _ in range(3):
+            out.fill_(np.nan)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
+            assert all(bool((j == 7.0).all()) for j in junk)
+        del graph
+    finally:
+        b.close()
+
+
 def test_stream_change_orders_work():
     """Calls from two torch streams on one context: the second stream waits
     for the first one's work, so the shared workspace is not raced."""
@@ -613,6 +658,89 @@ def test_matvec_nan_activation_poisons_rows(backend, encoding):
     backend.sync()
     assert np.isnan(orc.matvec(encoding, rows, columns, w, x)).all()
     assert np.isnan(out.cpu().numpy()).all()
+
+
+# Decode GEMV shapes of every M=1 route the integer-dot kernels take: the
+# DMA kernel (K = 5120 and 17408), the Q6_K odd-block tail workgroup (K =
+# 1280, 5 blocks per row) and the register kernel past the DMA kernel's LDS
+# (Q4_K, K = 24576).
+DECODE_ROUTES = [(8, 256, 5120), (12, 256, 5120), (13, 256, 5120), (14, 256, 5120), (23, 256, 5120),
+                 (12, 64, 17408), (14, 64, 17408), (14, 257, 1280), (12, 64, 24576)]
+
+
+@pytest.mark.parametrize("encoding,rows,columns", DECODE_ROUTES)
+@pytest.mark.parametrize("exp2", [-120, -100, 100])
+def test_matvec_extreme_activation_magnitudes(backend, encoding, rows, columns, exp2):
+    """x = N(0,1) * 2^exp2: the fixed-point slices use a power-of-two scale,
+    so small and large activations keep their relative precision. Checked
+    without the absolute 1e-6 allowance (it would hide any result at 2^-100):
+    per output |d| <= 4e-6 * sum|w*x|, and normwise <= 2e-3."""
+    import torch
+    w = quantized(encoding, rows, columns, 120)
+    x = (gaussian(121, columns) * np.float32(2.0 ** exp2)).astype(np.float32)
+    assert np.all(np.isfinite(x)) and np.abs(x).max() > 0
+    print(f"[extreme] enc {encoding} {rows}x{columns} x*2^{exp2}", flush=True)
+    out = torch.full((rows,), np.nan, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    got = out.cpu().numpy().astype(np.float64)
+    want = orc.matvec(encoding, rows, columns, w, x).astype(np.float64)
+    m = mass(encoding, w, rows, columns, x)[0]
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - want)
+    worst = int(np.argmax(err / m))
+    assert np.all(err <= F32_K * m), f"row {worst}: |d|={err[worst]:.3e} mass {m[worst]:.3e}"
+    assert err.max() / np.abs(want).max() <= 2e-3
+
+
+def _class_pattern(v):
+    """+1 for +Inf, -1 for -Inf, 2 for NaN, 0 for finite."""
+    v = np.asarray(v, np.float64)
+    return np.where(np.isnan(v), 2, np.where(np.isposinf(v), 1, np.where(np.isneginf(v), -1, 0)))
+
+
+INF_CASES = {
+    "pos": {1234: np.inf},
+    "neg": {77: -np.inf},
+    "both": {5: np.inf, 4000: -np.inf},
+    "same_slice": {64: np.inf, 65: np.inf, 95: -np.inf},
+    "inf_nan": {300: np.inf, 301: np.nan},
+}
+
+
+@pytest.mark.parametrize("encoding,rows,columns", DECODE_ROUTES)
+@pytest.mark.parametrize("case", sorted(INF_CASES))
+def test_matvec_infinite_activations_match_reference(backend, encoding, rows, columns, case):
+    """cpu.matvec multiplies each weight by its activation in F64
+    (backends/cpu/root.zig:144-152): an infinite activation makes a row +-Inf
+    by the sign of its weight, NaN where that weight is 0 or where products of
+    both signs meet; NaN stays NaN. The GPU output has the oracle's class in
+    every row (+Inf, -Inf, NaN), and its finite rows stay within the F32
+    bound."""
+    import torch
+    w = quantized(encoding, rows, columns, 130)
+    if encoding == 12 and case == "pos":
+        # make some weights of column 1234 exactly zero: group 4 of block 4
+        # gets scale 0 and minimum 0 in a few rows (bytes 4..15 hold them)
+        blk = w.reshape(rows, -1, 144)
+        blk[:8, 4, 4:16] = 0
+    x = gaussian(131, columns)
+    for c, v in INF_CASES[case].items():
+        x[c % columns] = v
+    print(f"[inf] enc {encoding} {rows}x{columns} {case}", flush=True)
+    out = torch.zeros(rows, device="cuda")
+    backend.matvec(nq.Matrix(encoding, rows, columns, to_gpu(w)), to_gpu(x), out)
+    backend.sync()
+    got = out.cpu().numpy()
+    want = orc.matvec(encoding, rows, columns, w, x)
+    np.testing.assert_array_equal(_class_pattern(got), _class_pattern(want))
+    assert not np.all(np.isfinite(want))
+    if encoding == 12 and case == "pos":
+        assert np.isnan(want[:8]).all() and np.isinf(want[8:]).all()  # the planted zeros reach NaN
+    fin = np.isfinite(want)
+    if fin.any():
+        xf = np.where(np.isfinite(x), x, 0).astype(np.float32)
+        check_close(got[fin], want[fin], mass(encoding, w, rows, columns, xf)[0][fin], F32_K, f"inf {encoding}")
 
 
 # Multi-token GEMV at F32 precision on the matrix cores (Q4_K / Q5_K, 2..3

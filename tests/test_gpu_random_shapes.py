@@ -56,7 +56,7 @@ def test_random_shape_matmul_matches_oracle(backend, encoding, rows, columns, to
     # F32 precision: the decode GEMV and the 2-3 token rows; the tiles round
     # activations (and some weights) to f16
     k = F32_K if xdtype == "f32" and tokens <= 3 else F16_K
-    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, f"random {encoding}")
+    check_close(out.cpu().numpy(), want, mass(encoding, w, rows, columns, xref), k, f"random {encoding} {rows}x{columns} M={tokens} {xdtype} seed {seed}")
 
 
 def gemv_cases(n=24, seed=77):
@@ -84,7 +84,7 @@ def test_random_shape_matvec_matches_oracle(backend, encoding, rows, columns, se
     backend.sync()
     want = orc.matvec(encoding, rows, columns, w, x)
     check_close(out.cpu().numpy()[None, :], want[None, :], mass(encoding, w, rows, columns, x[None, :]), F32_K,
-                f"random gemv {encoding}")
+                f"random-gemv {encoding} {rows}x{columns} seed {seed}")
 
 
 def strided_cases(n=14, seed=4242):
@@ -129,4 +129,4 @@ def test_random_strided_matmul_matches_oracle(backend, encoding, rows, columns, 
     assert np.isnan(got[:, rows:]).all(), "output padding was written"
     want = orc.matmul(encoding, rows, columns, w, np.ascontiguousarray(xref))
     k = F32_K if xdtype == "f32" and tokens <= 3 else F16_K
-    check_close(got[:, :rows], want, mass(encoding, w, rows, columns, xref), k, f"strided {encoding}")
+    check_close(got[:, :rows], want, mass(encoding, w, rows, columns, xref), k, f"strided {encoding} {rows}x{columns} M={tokens} {xdtype} seed {seed}")
