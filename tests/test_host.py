@@ -165,3 +165,26 @@ def test_gemv_asm_loads_are_not_read_before_their_waits():
         count, found = hazards(out.read_text())
     assert count >= 10, count
     assert not found, found[:5]
+
+
+def test_asm_hazard_checker_catches_planted_races():
+    """The static checker itself: reads and writes of an in-flight load's
+    registers before its wait are reported, vmcnt(N) retires only the older
+    loads, and a load at the bottom of a loop is checked against the top."""
+    from tests.isa.asm_hazard import hazards
+
+    def run(body):
+        asm = "_ZN3nuq15gemv_dma_kernelX:  ; @k\n" + "\n".join(body) + "\n.Lfunc_end0:\n"
+        return hazards(asm)[1]
+
+    load_a = "global_load_dwordx4 v[0:3], v[20:21], off"
+    load_b = "global_load_dwordx4 v[4:7], v[22:23], off"
+    assert run([load_a, "s_waitcnt vmcnt(0)", "v_add_u32_e32 v8, v0, v1"]) == []
+    assert run([load_a, "v_add_u32_e32 v8, v0, v1", "s_waitcnt vmcnt(0)"])        # read before the wait
+    assert run([load_a, "v_mov_b32_e32 v2, 0", "s_waitcnt vmcnt(0)"])             # write before the wait
+    assert run([load_a, load_b, "s_waitcnt vmcnt(1)", "v_add_u32_e32 v8, v0, v1"]) == []
+    assert run([load_a, load_b, "s_waitcnt vmcnt(1)", "v_add_u32_e32 v8, v4, v1"])  # b still in flight
+    assert run([load_a, "global_load_lds_dwordx4 v[20:21], off", "s_waitcnt vmcnt(1)",
+                "v_add_u32_e32 v8, v0, v1"]) == []                                  # the copy writes no VGPR
+    assert run([".LBB0_1:", "v_add_u32_e32 v8, v0, v1", "s_waitcnt vmcnt(0)", load_a,
+                "s_cbranch_scc1 .LBB0_1", "s_waitcnt vmcnt(0)"])                     # loop back edge
