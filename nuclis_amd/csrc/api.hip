@@ -297,6 +297,16 @@ int matmul_impl(nuq_context *ctx, uint32_t kernel, const nuq_matrix *m, const vo
     // measurement aid, as the reference's matmulKernel forces a kernel).
     if (kernel == NUQ_KERNEL_ROWS && !specialised(m->encoding))
         return run_generic(ctx, m, stride, x, f16, in_stride, out, out_stride, tokens);
+    if (kernel == NUQ_KERNEL_ROWS && f16 && m->encoding == NUQ_Q4_K) {
+        // the K-split register kernel; rows longer than 24 blocks run as K
+        // ranges into the workspace (at most 4 ranges)
+        if (m->columns > 24 * 256) (void)ensure_workspace(ctx, 4ull * tokens * m->rows);
+        hipError_t le = hipSuccess;
+        if (nuq::launch_rows_q4k_f16(ctx->stream, (const uint8_t *)m->bytes, stride, (uint32_t)m->rows,
+                                     (uint32_t)m->columns, (const _Float16 *)x, in_stride, out, out_stride, tokens,
+                                     ctx->split.work, (uint64_t)ctx->split.tiles * 256 * 256, &le))
+            return hip_check(ctx, le, "multi-token gemv launch");
+    }
     if (kernel == NUQ_KERNEL_ROWS)
         return hip_check(ctx,
                          nuq::launch_rows(ctx->stream, m->encoding, (const uint8_t *)m->bytes, stride,

@@ -2134,6 +2134,14 @@ __global__ void verify_reduce_kernel(const float *__restrict__ ws, uint32_t nran
     y[(uint64_t)t * out_stride + r] = v;
 }
 
+hipError_t launch_verify_reduce(hipStream_t s, const float *ws, uint32_t ranges, uint32_t rows, uint32_t tokens,
+                                float *y, uint64_t out_stride) {
+    const uint32_t n = rows * tokens;
+    hipLaunchKernelGGL(verify_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, ws, ranges, rows, tokens, y,
+                       out_stride);
+    return hipGetLastError();
+}
+
 // Streams when the row's blocks fit 12 waves of at most 2 blocks, or, with a
 // workspace, in K ranges of at most 24 blocks whose sums verify_reduce_kernel
 // adds; returns false (nothing launched) otherwise.

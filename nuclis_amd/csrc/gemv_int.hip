@@ -1272,4 +1272,326 @@ hipError_t launch_gemv_dma_segments(hipStream_t s, uint32_t encoding, uint32_t c
     return hipErrorInvalidValue;
 }
 
+
+// ---------------------------------------------------------------------------
+// Register-dequant multi-token GEMV (matvecRows form, backends/metal/kernels/
+// matvec_rows.metal:34-130: decode each weight once, dot it with every token)
+// for Q4_K with f16 activations, 1..8 tokens: KERNEL_ROWS.
+//
+// Each weight is decoded once into registers as the exact f16 integer q*sc
+// (at most 15*63 = 945) and meets every token's f16 activations in
+// v_dot2_f32_f16 (two exact products per op, F32 accumulation), so the
+// products are exact and only the F32 sums round, as in an F32 FMA chain;
+// the block's d and the minimum term dmin*m*sum(x) are applied in F32.
+//
+// Layout: the K-split of the decode GEMV. Lane = (block slot 0..7, sub s
+// 0..7): s / 2 is the block's nibble pair j (groups 2j and 2j+1), and the
+// lane takes code bytes 16*(s%2) .. +15 of the pair, i.e. 16 values of each
+// of the two groups. Wave kw of a wave set owns blocks [8kw, 8kw + 8) of
+// every row of its K range, so each lane keeps its 32 activations of every
+// token in registers (16 f16 pairs per token) with their per-group F32 sums
+// for the whole launch. A step is 4 rows x the wave's 8 blocks, copied
+// global -> LDS into a private two-slot ring as the decode GEMV copies its
+// steps; the lanes then take the 4 rows in turn. A row's token partials are
+// reduced across the wave with a reduce-scatter (each row-swap or DPP stage
+// halves the values a lane holds), so lane (64 / NT) * t ends with token t's
+// sum; per-wave partials meet in LDS and are added in wave order. Rows
+// longer than 24 blocks run as K ranges (blockIdx.y) whose sums
+// verify_reduce_kernel adds.
+
+// 8 tokens hold 128 registers of activations: 8 waves (256 registers) there
+template <int NT>
+constexpr int rd_threads() { return NT == 8 ? 512 : NT == 4 ? 768 : 1024; }
+constexpr uint32_t RD_ROW_CHUNKS = 8 * 144 / 16;                        // 72: a row's 8 blocks
+constexpr uint32_t RD_INSTRS = (4 * RD_ROW_CHUNKS + 63) / 64;           // 5 copies per 4-row step
+constexpr uint32_t RD_SLOT_BYTES = RD_INSTRS * 1024;
+
+typedef _Float16 rd_half2_t __attribute__((ext_vector_type(2)));
+
+template <int CTRL>
+__device__ __forceinline__ float rd_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the wave's 64 lanes of each of a lane's NT token values, as a
+// reduce-scatter: each stage halves the values a lane holds, the lanes
+// whose bit is clear keeping the first half. Bits 32 and 16 swap rows with
+// v_permlane32_swap / v_permlane16_swap (one swap and one add per value),
+// bit 8 pairs lanes with a DPP row mirror; the lanes left holding one token
+// then add the rest of their group. Returns the total of token
+// (lane / (64 / NT)) % NT, held by every lane of that group.
+__device__ __forceinline__ void rd_swap32(float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ void rd_swap16(float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+template <int NT>
+__device__ __forceinline__ float rd_reduce(float *v, uint32_t lane) {
+#pragma unroll
+    for (int k = 0; k < NT / 2; ++k) rd_swap32(v[k], v[k + NT / 2]);
+    if constexpr (NT >= 4) {
+#pragma unroll
+        for (int k = 0; k < NT / 4; ++k) rd_swap16(v[k], v[k + NT / 4]);
+    }
+    float r = v[0];
+    if constexpr (NT == 8) {  // bit 8: row_mirror pairs lane i with 15 - i
+        const bool lower = (lane & 8) == 0;
+        const float send = lower ? v[1] : v[0], keep = lower ? v[0] : v[1];
+        r = keep + rd_dpp<0x140>(send);
+    }
+    if constexpr (NT == 2) {  // the other half of the 32 lanes
+        float t = r;
+        rd_swap16(r, t);
+    }
+    if constexpr (NT <= 4) r += rd_dpp<0x140>(r);  // row_mirror
+    r += rd_dpp<0x141>(r);                       // row_half_mirror
+    r += rd_dpp<0x4e>(r);                        // quad_perm [2,3,0,1]
+    r += rd_dpp<0xb1>(r);                        // quad_perm [1,0,3,2]
+    return r;
+}
+
+// q*sc of 4 low (or high) nibbles as two exact f16 pairs: bytes (1024 + q)
+// via v_perm_b32 from the nibble word and 0x64 bytes, then (1024 + q)*sc -
+// 1024*sc in one v_pk_fma_f16 (the product is exact before the one rounding).
+__device__ __forceinline__ void rd_codes(uint32_t nib, rd_half2_t sc, rd_half2_t nsc, rd_half2_t &p0, rd_half2_t &p1) {
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u);
+    p0 = __builtin_elementwise_fma(__builtin_bit_cast(rd_half2_t, a), sc, nsc);
+    p1 = __builtin_elementwise_fma(__builtin_bit_cast(rd_half2_t, b), sc, nsc);
+}
+
+template <int NT>
+__global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_t *__restrict__ w, uint64_t stride,
+                                                                      uint32_t rows, uint32_t nblocks_all,
+                                                                      uint32_t ranges, uint32_t rows_per_wg,
+                                                                      uint32_t set_waves,
+                                                                      const _Float16 *__restrict__ x,
+                                                                      uint64_t in_stride, uint32_t tokens,
+                                                                      float *__restrict__ y, uint64_t out_stride) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    constexpr uint32_t BYTES = 144, ROW_CHUNKS = RD_ROW_CHUNKS, INSTRS = RD_INSTRS;
+    const uint32_t range = blockIdx.y;
+    const uint32_t b0 = range * nblocks_all / ranges, kb = (range + 1) * nblocks_all / ranges - b0;
+    w += (uint64_t)b0 * BYTES;
+    x += (uint64_t)b0 * 256;
+
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t nwaves = blockDim.x >> 6;
+    uint8_t *ring = (uint8_t *)lds + wv * 2 * RD_SLOT_BYTES;
+    float *partial = (float *)(lds + nwaves * 2 * (RD_SLOT_BYTES / 4));  // rows_per_wg * set_waves * NT + nwaves * 64
+    const uint32_t sets = nwaves / set_waves;
+    const uint32_t set = wv / set_waves, kw = wv % set_waves;
+    const uint32_t slot = lane >> 3, sub = lane & 7, j = sub >> 1, c0 = 16 * (sub & 1);
+    const bool direct = j < 2;
+    const uint32_t shift = direct ? 16 * j : 16 * j - 32;
+    const uint32_t b = 8 * kw + slot;
+    const bool live = b < kb;
+    const uint32_t row_begin = blockIdx.x * rows_per_wg;
+    const uint32_t row_end = min(row_begin + rows_per_wg, rows);
+    const uint32_t first = row_begin + set * 4;
+    const uint32_t set_stride = sets * 4;
+    const uint32_t nsteps = first < row_end ? (row_end - first + set_stride - 1) / set_stride : 0;
+
+    // DMA: lane i of copy n moves chunk 64n + i of the step (4 rows x 8 blocks)
+    uint32_t dq[INSTRS], doff[INSTRS];
+#pragma unroll
+    for (uint32_t n = 0; n < INSTRS; ++n) {
+        const uint32_t k = min(64 * n + lane, 4 * ROW_CHUNKS - 1);
+        const uint32_t off = 8 * kw * BYTES + 16 * (k % ROW_CHUNKS);
+        dq[n] = k / ROW_CHUNKS;
+        doff[n] = off < kb * BYTES ? off : 0;
+    }
+    const uint8_t *wg_base = w + (uint64_t)row_begin * stride;
+    const uint32_t stride32 = (uint32_t)stride;
+    const uint32_t first_local = first - row_begin, last_local = row_end - 1 - row_begin;
+#define NUQ_RD_DMA(SLOT_, STEP_)                                                                           \
+    _Pragma("unroll") for (uint32_t n = 0; n < INSTRS; ++n) {                                              \
+        const uint32_t lrow_ = min(first_local + (STEP_) * set_stride + dq[n], last_local);                \
+        __builtin_amdgcn_global_load_lds((gd_global_void_t *)(wg_base + (lrow_ * stride32 + doff[n])),     \
+                                         (gd_lds_void_t *)(ring + (SLOT_) * RD_SLOT_BYTES + n * 1024), 16, 0, 2); \
+    }
+    NUQ_RD_DMA(0, 0u)
+    NUQ_RD_DMA(1, 1u)
+
+    // this lane's 16 + 16 activations of every token, and their F32 sums
+    uint4 xa[NT][2], xb[NT][2];
+    float sa_x[NT], sb_x[NT];
+    {
+        const uint32_t col = (live ? b : 0) * 256 + 64 * j + c0;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const _Float16 *p = x + (uint64_t)min((uint32_t)t, tokens - 1) * in_stride + col;
+            xa[t][0] = *(const uint4 *)p;
+            xa[t][1] = *(const uint4 *)(p + 8);
+            xb[t][0] = *(const uint4 *)(p + 32);
+            xb[t][1] = *(const uint4 *)(p + 40);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            // group sums: 1*x0 + 1*x1 per v_dot2_f32_f16, the products exact
+            const rd_half2_t one = {(_Float16)1.f, (_Float16)1.f};
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if ((uint32_t)t >= tokens || !live) xa[t][h] = xb[t][h] = make_uint4(0, 0, 0, 0);
+                const uint32_t wa[4] = {xa[t][h].x, xa[t][h].y, xa[t][h].z, xa[t][h].w};
+                const uint32_t wb[4] = {xb[t][h].x, xb[t][h].y, xb[t][h].z, xb[t][h].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(rd_half2_t, wa[k]), one, s0, false);
+                    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(rd_half2_t, wb[k]), one, s1, false);
+                }
+            }
+            sa_x[t] = s0;
+            sb_x[t] = s1;
+        }
+    }
+    const uint32_t spare = rows_per_wg * set_waves * NT + wv * 64;
+    const uint32_t hdr_base = lds_u8_addr(ring) + slot * BYTES;
+    const uint32_t code_base = hdr_base + 16 + 32 * j + c0;
+
+    // A row's header and code chunk are read from the ring one row ahead
+    // (the first row of a step right after its copies land), so the LDS
+    // latency of row q + 1 hides under row q's arithmetic.
+    u32x4_t hn_, cn_;
+#define NUQ_RD_READ(SLOT_, Q_)                                                                              \
+    asm volatile("ds_read_b128 %0, %2 offset:%4\n\t"                                                        \
+                 "ds_read_b128 %1, %3 offset:%4"                                                            \
+                 : "=&v"(hn_), "=&v"(cn_)                                                                   \
+                 : "v"(hdr_base), "v"(code_base), "n"((SLOT_) * RD_SLOT_BYTES + (Q_) * (ROW_CHUNKS * 16))   \
+                 : "memory");
+#define NUQ_RD_ROW(SLOT_, STEP_, Q_, NEXT_)                                                                 \
+    {                                                                                                       \
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(hn_), "+v"(cn_) : : "memory");                           \
+        const u32x4_t h_ = hn_, c_ = cn_;                                                                   \
+        NEXT_                                                                                               \
+        /* lanes past the row's last block read arbitrary copied bytes: their d and dmin are zero (their */ \
+        /* activations are zero too, and the q*sc from any bytes are finite) */                             \
+        const float d_ = live ? half_bits(h_.x & 0xffffu) : 0.f;                                            \
+        const float dmin_ = live ? half_bits(h_.x >> 16) : 0.f;                                             \
+        float sa_, ma_, sb_, mb_;                                                                           \
+        q4k_pair_f(h_.y, h_.z, h_.w, shift, direct, sa_, ma_, sb_, mb_);                                    \
+        const float dma_ = -(dmin_ * ma_), dmb_ = -(dmin_ * mb_);                                           \
+        const rd_half2_t sca_ = {(_Float16)sa_, (_Float16)sa_}, scb_ = {(_Float16)sb_, (_Float16)sb_};      \
+        const rd_half2_t nsa_ = sca_ * (_Float16)-1024.f, nsb_ = scb_ * (_Float16)-1024.f;                   \
+        const uint32_t cw_[4] = {c_.x, c_.y, c_.z, c_.w};                                                   \
+        rd_half2_t wa_[8], wb_[8];                                                                          \
+        _Pragma("unroll") for (int k = 0; k < 4; ++k) {                                                     \
+            rd_codes(cw_[k] & 0x0f0f0f0fu, sca_, nsa_, wa_[2 * k], wa_[2 * k + 1]);                         \
+            rd_codes((cw_[k] >> 4) & 0x0f0f0f0fu, scb_, nsb_, wb_[2 * k], wb_[2 * k + 1]);                  \
+        }                                                                                                   \
+        float v_[NT];                                                                                       \
+        _Pragma("unroll") for (int t = 0; t < NT; ++t) {                                                    \
+            float acc = 0.f;                                                                                \
+            _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                                 \
+                acc = __builtin_amdgcn_fdot2(wa_[4 * h + 0], __builtin_bit_cast(rd_half2_t, xa[t][h].x), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wa_[4 * h + 1], __builtin_bit_cast(rd_half2_t, xa[t][h].y), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wa_[4 * h + 2], __builtin_bit_cast(rd_half2_t, xa[t][h].z), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wa_[4 * h + 3], __builtin_bit_cast(rd_half2_t, xa[t][h].w), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wb_[4 * h + 0], __builtin_bit_cast(rd_half2_t, xb[t][h].x), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wb_[4 * h + 1], __builtin_bit_cast(rd_half2_t, xb[t][h].y), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wb_[4 * h + 2], __builtin_bit_cast(rd_half2_t, xb[t][h].z), acc, false); \
+                acc = __builtin_amdgcn_fdot2(wb_[4 * h + 3], __builtin_bit_cast(rd_half2_t, xb[t][h].w), acc, false); \
+            }                                                                                               \
+            v_[t] = fmaf(d_, acc, fmaf(dma_, sa_x[t], dmb_ * sb_x[t]));                                     \
+        }                                                                                                   \
+        const float tot_ = rd_reduce<NT>(v_, lane);                                                         \
+        const uint32_t row_ = first + (STEP_) * set_stride + (Q_);                                          \
+        /* lane (64 / NT) t holds token t's total; the other lanes write to this wave's spare words */     \
+        const bool writer_ = (lane & (64 / NT - 1)) == 0 && row_ < row_end;                                 \
+        partial[writer_ ? ((row_ - row_begin) * set_waves + kw) * NT + lane / (64 / NT) : spare + lane] = tot_; \
+    }
+    // Step i lives in ring slot i % 2; a slot is refilled with step i + 2
+    // once its 4 rows are read.
+#define NUQ_RD_STEP(SLOT_, STEP_, VM_, REFILL_)                                                              \
+    {                                                                                                        \
+        asm volatile("s_waitcnt vmcnt(%0)" : : "n"(VM_) : "memory");                                        \
+        NUQ_RD_READ(SLOT_, 0)                                                                                \
+        NUQ_RD_ROW(SLOT_, STEP_, 0, NUQ_RD_READ(SLOT_, 1))                                                   \
+        NUQ_RD_ROW(SLOT_, STEP_, 1, NUQ_RD_READ(SLOT_, 2))                                                   \
+        NUQ_RD_ROW(SLOT_, STEP_, 2, NUQ_RD_READ(SLOT_, 3))                                                   \
+        NUQ_RD_ROW(SLOT_, STEP_, 3, )                                                                        \
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); /* the slot's reads are done */                \
+        REFILL_                                                                                              \
+    }
+    // the x loads were issued after the first two steps' copies: wait for all
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    uint32_t i = 0;
+    for (; i + 4 <= nsteps; i += 2) {
+        NUQ_RD_STEP(0, i, INSTRS, NUQ_RD_DMA(0, i + 2))
+        NUQ_RD_STEP(1, i + 1, INSTRS, NUQ_RD_DMA(1, i + 3))
+    }
+    if (i < nsteps) NUQ_RD_STEP(0, i, 0, if (i + 2 < nsteps) { NUQ_RD_DMA(0, i + 2) })
+    if (i + 1 < nsteps) NUQ_RD_STEP(1, i + 1, 0, if (i + 3 < nsteps) { NUQ_RD_DMA(1, i + 3) })
+    if (i + 2 < nsteps) NUQ_RD_STEP(0, i + 2, 0, )
+    if (i + 3 < nsteps) NUQ_RD_STEP(1, i + 3, 0, )
+#undef NUQ_RD_STEP
+#undef NUQ_RD_ROW
+#undef NUQ_RD_READ
+#undef NUQ_RD_DMA
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // copies issued for steps past the range land before the end
+    __syncthreads();
+    const uint32_t n = (row_end - row_begin) * tokens;
+    for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
+        const uint32_t t = e / (row_end - row_begin), r = e % (row_end - row_begin);
+        float v = 0.f;
+        for (uint32_t k = 0; k < set_waves; ++k) v += partial[(r * set_waves + k) * NT + t];
+        if (ranges == 1) y[(uint64_t)t * out_stride + row_begin + r] = v;
+        else y[((uint64_t)range * tokens + t) * rows + row_begin + r] = v;
+    }
+}
+
+// KERNEL_ROWS for Q4_K with f16 activations (1..8 tokens). `ws` (rows *
+// tokens * ranges floats, or null) takes the K ranges of rows longer than
+// 24 blocks. Returns false (nothing launched) for shapes it does not take.
+bool launch_rows_q4k_f16(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
+                         const _Float16 *x, uint64_t in_stride, float *y, uint64_t out_stride, uint32_t tokens,
+                         float *ws, uint64_t ws_floats, hipError_t *err) {
+    if (tokens < 1 || tokens > 8 || columns % 256 != 0 || rows < 4) return false;
+    if (((uintptr_t)x & 15) != 0 || (in_stride * 2) % 16 != 0) return false;
+    const uint32_t nb = columns / 256;
+    // K ranges: one when a wave set (8 blocks per wave) holds the row in at
+    // most 3 waves, else the range count up to 4 with the fewest idle block
+    // slots (68 blocks: 3 ranges of 22-23 blocks, 3 waves each)
+    uint32_t ranges = 0, best_waste = ~0u;
+    for (uint32_t r = 1; r <= 4; ++r) {
+        const uint32_t kb = (nb + r - 1) / r, sw = (kb + 7) / 8;
+        if (sw > 3) continue;
+        const uint32_t waste = sw * 8 * r - nb;
+        if (ranges == 0 || waste < best_waste) {
+            ranges = r;
+            best_waste = waste;
+        }
+        if (r == 1) break;  // one range needs no reduce pass
+    }
+    if (ranges == 0) return false;
+    if (ranges > 1 && (!ws || (uint64_t)ranges * tokens * rows > ws_floats)) return false;
+    const uint32_t set_waves = ((nb + ranges - 1) / ranges + 7) / 8;
+    const uint32_t nt = tokens <= 2 ? 2 : tokens <= 4 ? 4 : 8;
+    const uint32_t max_waves = (nt == 8 ? rd_threads<8>() : nt == 4 ? rd_threads<4>() : rd_threads<2>()) / 64;
+    const uint32_t sets = std::max(1u, max_waves / set_waves);
+    const uint32_t nwaves = sets * set_waves;
+    const uint32_t wgs = std::max(1u, 256 / ranges);
+    const uint32_t rows_per_wg = std::max(4u, (rows + wgs - 1) / wgs);
+    if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return false;
+    const size_t lds = (size_t)nwaves * 2 * RD_SLOT_BYTES + ((size_t)rows_per_wg * set_waves * nt + nwaves * 64) * 4;
+    if (lds > 160 * 1024) return false;
+    const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg, ranges), block(64 * nwaves);
+    float *out = ranges > 1 ? ws : y;
+#define NUQ_RD_LAUNCH(NT_)                                                                                   \
+    hipLaunchKernelGGL((rows_dma_kernel<NT_>), grid, block, lds, s, w, stride, rows, nb, ranges, rows_per_wg, \
+                       set_waves, x, in_stride, tokens, out, out_stride)
+    if (nt == 2) NUQ_RD_LAUNCH(2);
+    else if (nt == 4) NUQ_RD_LAUNCH(4);
+    else NUQ_RD_LAUNCH(8);
+#undef NUQ_RD_LAUNCH
+    *err = hipGetLastError();
+    if (*err == hipSuccess && ranges > 1) *err = launch_verify_reduce(s, ws, ranges, rows, tokens, y, out_stride);
+    return true;
+}
+
 }  // namespace nuq

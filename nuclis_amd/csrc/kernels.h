@@ -77,6 +77,17 @@ hipError_t launch_tile(hipStream_t s, uint32_t encoding, const uint8_t *w, uint6
                        uint32_t columns, const void *x, uint32_t x_f16, uint64_t in_stride, float *y,
                        uint64_t out_stride, uint32_t tokens, const SplitScratch &scratch);
 uint32_t split_scratch_tiles();
+// Adds `ranges` K-range partial outputs ws[(k * tokens + t) * rows + r] in
+// range order into y[t * out_stride + r].
+hipError_t launch_verify_reduce(hipStream_t s, const float *ws, uint32_t ranges, uint32_t rows, uint32_t tokens,
+                                float *y, uint64_t out_stride);
+// Register-dequant multi-token GEMV (KERNEL_ROWS) for Q4_K with f16
+// activations, 1..8 tokens; `ws` (ws_floats floats) takes the K ranges of
+// rows longer than 24 blocks. False (nothing launched) for shapes it does
+// not take; otherwise *err is the launch status.
+bool launch_rows_q4k_f16(hipStream_t s, const uint8_t *w, uint64_t stride, uint32_t rows, uint32_t columns,
+                         const _Float16 *x, uint64_t in_stride, float *y, uint64_t out_stride, uint32_t tokens,
+                         float *ws, uint64_t ws_floats, hipError_t *err);
 // Multi-token GEMV of F32 activations (1..4 tokens) at F32 precision on the
 // matrix cores (the streamed verify tile with each token's activations as
 // three f16 parts); Q4_K / Q5_K. *taken is false (and nothing launched)

@@ -915,3 +915,33 @@ def test_matvec_rows_f16_matches_oracle(backend, encoding, rows, columns, tokens
     m_ = mass(encoding, w, rows, columns, x)
     check_close(out.cpu().numpy(), want, m_, F32_K, f"rows-f16 {encoding}")
     check_close(auto.cpu().numpy(), want, m_, F32_K, f"auto-f16 {encoding}")
+
+
+# The K-split register-dequant kernel behind KERNEL_ROWS for Q4_K with f16
+# activations (1..8 tokens): one K range up to 32 blocks, K ranges (and the
+# range reduce) beyond; rows that are not whole 4-row steps; rows with fewer
+# blocks than a wave's 4; padded activation and output strides. Every product
+# is exact (f16 activations times the exact f16 integer q * sc), so the plain
+# F32 bound holds.
+RD_SHAPES = [(17408, 5120), (5120, 17408), (1000, 256), (40, 1280), (264, 12288), (520, 8448)]
+
+
+@pytest.mark.parametrize("rows,columns", RD_SHAPES)
+@pytest.mark.parametrize("tokens", [1, 2, 3, 5, 8])
+def test_register_rows_kernel_f16_matches_oracle(backend, rows, columns, tokens):
+    import torch
+    w = quantized(12, rows, columns, 150 + tokens)
+    in_stride, out_stride = columns + 8, rows + 4
+    x16 = np.zeros((tokens, in_stride), np.float16)
+    x16[:, :columns] = gaussian(151 + tokens, (tokens, columns)).astype(np.float16)
+    m = nq.Matrix(12, rows, columns, to_gpu(w))
+    print(f"[rows-dma] {rows}x{columns} T={tokens}", flush=True)
+    out = torch.full((tokens, out_stride), np.nan, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_ROWS, m, to_gpu(x16), in_stride, out, out_stride, tokens)
+    backend.sync()
+    got = out.cpu().numpy()
+    assert np.isnan(got[:, rows:]).all(), "output padding was written"
+    x = x16[:, :columns].astype(np.float32)
+    want = orc.matmul(12, rows, columns, w, x)
+    check_close(got[:, :rows], want, mass(12, w, rows, columns, x), F32_K,
+                f"rows-dma {rows}x{columns} T={tokens}")
