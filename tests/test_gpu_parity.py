@@ -945,3 +945,36 @@ def test_register_rows_kernel_f16_matches_oracle(backend, rows, columns, tokens)
     want = orc.matmul(12, rows, columns, w, x)
     check_close(got[:, :rows], want, mass(12, w, rows, columns, x), F32_K,
                 f"rows-dma {rows}x{columns} T={tokens}")
+
+
+@pytest.mark.parametrize("rows,columns,tokens", [(5120, 17408, 8), (17408, 5120, 3)])
+def test_register_rows_kernel_graph_replays_match_eager(backend, rows, columns, tokens):
+    """The register-dequant kernel captured in a HIP graph (its K ranges and
+    range reduce included) replays bit-identically to the eager call, with
+    eager work between the replays."""
+    import torch
+    w = quantized(12, rows, columns, 160)
+    xg = to_gpu(gaussian(161, (tokens, columns)).astype(np.float16))
+    m = nq.Matrix(12, rows, columns, to_gpu(w))
+    print(f"[rows-dma graph] {rows}x{columns} T={tokens}", flush=True)
+    eager = torch.full((tokens, rows), np.nan, device="cuda")
+    backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, eager, rows, tokens)  # sizes the workspace
+    backend.sync()
+    out = torch.full((tokens, rows), np.nan, device="cuda")
+    other = torch.empty((tokens, rows), device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, out, rows, tokens)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(np.nan)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
+        backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, other, rows, tokens)
+        backend.sync()
+        assert torch.equal(other.view(torch.int32), eager.view(torch.int32))
