@@ -868,7 +868,9 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     const uint32_t nwaves = blockDim.x >> 6;
     uint8_t *rings = (uint8_t *)lds;                                          // nwaves * D * GD_SLOT_BYTES
     uint32_t *slices = lds + nwaves * D * (GD_SLOT_BYTES / 4);                // nslices * SLICE_WORDS
-    float *partial = (float *)(slices + nslices * SLICE_WORDS);               // rows_per_wg * set_waves + nwaves
+    // rows_per_wg * set_waves partial sums, one spare per wave, then one
+    // row-step counter per K range
+    float *partial = (float *)(slices + nslices * SLICE_WORDS);
     uint8_t *ring = rings + wv * D * GD_SLOT_BYTES;
 #define NUQ_GD_RING(SLOT_) (ring + (SLOT_) * GD_SLOT_BYTES)
     const uint32_t sets = nwaves / set_waves;
@@ -974,6 +976,8 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
         xhalf_wait<0>(xh);
         quantize_half_slice<true>(xh, t & 1, slices + (t >> 1) * SLICE_WORDS);
     }
+    // the row-step counters of the K ranges (D * sets steps are assigned statically)
+    if (t0 < set_waves) ((uint32_t *)(partial + rows_per_wg * set_waves + nwaves))[t0] = D * sets;
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     __builtin_amdgcn_s_barrier();
     }
@@ -996,11 +1000,11 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
     const uint32_t role = g * ROW_CHUNKS * 16 + slot * BYTES;
     const uint32_t spare = rows_per_wg * set_waves + wv;  // one spare partial per wave
 
-    // Step i lives in ring slot i % D. As soon as a slot's bytes are in
-    // registers the slot is refilled with step i + D, before the arithmetic.
-    // In the main loop the D-1 younger steps' copies (3 each) may still be in
-    // flight when slot d is read; the peeled tail issues fewer copies, so it
-    // waits for all of them.
+    // Each ring slot holds one step. As soon as a slot's bytes are in
+    // registers the slot is refilled with the wave's next step, before the
+    // arithmetic. While every slot is refilled, the D-1 younger steps'
+    // copies may still be in flight when slot d is read; once refills stop,
+    // the remaining slots wait for all copies.
 #define NUQ_GD_COMPUTE(SLOT_, STEP_, VM_, REFILL_)                                                                     \
     {                                                                                                       \
         GdEnc<ENC> e_;                                                                                      \
@@ -1012,6 +1016,58 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
         /* every lane of the group holds the sum; rows past the range go to a spare slot */               \
         partial[row < row_end ? (row - row_begin) * set_waves + kw : spare] = v;                            \
     }
+    if constexpr (!WX) {
+#define NUQ_GD_DMA2(SLOT_, C_)                                                                                \
+    _Pragma("unroll") for (uint32_t n = 0; n < GD_DMA_INSTRS; ++n) {                                          \
+        const uint32_t lrow_ = min((C_) * GROUPS + dq[n], last_local);                                        \
+        __builtin_amdgcn_global_load_lds((gd_global_void_t *)(wg_base + (lrow_ * stride32 + doff[n])),        \
+                                         (gd_lds_void_t *)(NUQ_GD_RING(SLOT_) + n * 1024), 16, 0, 2);         \
+    }
+#define NUQ_GD_COMPUTE2(SLOT_, C_, VM_, REFILL_)                                                            \
+    {                                                                                                       \
+        GdEnc<ENC> e_;                                                                                      \
+        e_.template read<VM_>(NUQ_GD_RING(SLOT_) + role, j);                                                \
+        REFILL_                                                                                             \
+        const float v = group_sum<4 * SLOTS>(live ? e_.dot(xa, xb, j, shift, direct) : 0.f);                \
+        const uint32_t row = row_begin + (C_) * GROUPS + g;                                                 \
+        partial[row < row_end ? (row - row_begin) * set_waves + kw : spare] = v;                            \
+    }
+        // Waves of one K range (one per wave set) claim row steps from a
+        // shared LDS counter, so waves that start late take fewer steps.
+        const uint32_t tsteps = (row_end - row_begin + GROUPS - 1) / GROUPS;
+        const uint32_t claim_addr =
+            lds_u8_addr((const uint8_t *)(partial + rows_per_wg * set_waves + nwaves + kw));
+        uint32_t sid[D];
+        bool claiming = true;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            sid[d] = set + d * sets;
+            if (sid[d] >= tsteps) claiming = false;
+        }
+        while (claiming) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                if (claiming) {
+                    // The claim is issued before the ring read, whose
+                    // lgkmcnt(0) also covers it (asm: the compiler would
+                    // wait for every copy before an LDS atomic).
+                    uint32_t c_ = 0;
+                    if (lane == 0)
+                        asm volatile("ds_add_rtn_u32 %0, %1, %2" : "=v"(c_) : "v"(claim_addr), "v"(1u) : "memory");
+                    NUQ_GD_COMPUTE2(d, sid[d], GD_DMA_INSTRS * (D - 1),
+                                    asm volatile("" : "+v"(c_));
+                                    c_ = __builtin_amdgcn_readfirstlane(c_);
+                                    if (c_ < tsteps) { NUQ_GD_DMA2(d, c_) } else claiming = false;)
+                    sid[d] = c_;
+                }
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (sid[d] < tsteps) NUQ_GD_COMPUTE2(d, sid[d], 0, )
+#undef NUQ_GD_COMPUTE2
+#undef NUQ_GD_DMA2
+    } else {  // one wave set: each K range has one wave, steps in order
     uint32_t i = 0;
     for (; i + 2 * D <= nsteps; i += D) {
 #pragma unroll
@@ -1026,6 +1082,7 @@ __global__ void __launch_bounds__(gd_threads<ENC>()) gemv_dma_kernel(const uint8
 #pragma unroll
     for (int d = 0; d < D; ++d)
         if (i + D + d < nsteps) NUQ_GD_COMPUTE(d, i + D + d, 0, )
+    }
 #undef NUQ_GD_COMPUTE
 #undef NUQ_GD_DMA
 #undef NUQ_GD_RING
@@ -1079,7 +1136,7 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     auto lds_for = [&](uint32_t st) {
         const size_t wv = (size_t)set_waves * st;
         return wv * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
-               ((size_t)rows_per_wg * set_waves + wv) * 4;
+               ((size_t)rows_per_wg * set_waves + wv + set_waves) * 4;
     };
     while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
     const uint32_t waves = set_waves * sets;
@@ -1140,7 +1197,7 @@ static hipError_t launch_dma_segments(hipStream_t s, uint32_t count, const uint8
     auto lds_for = [&](uint32_t st) {
         const size_t wv = (size_t)set_waves * st;
         return wv * D * GdEnc<ENC>::INSTRS * 1024 + (size_t)nblocks * 8 * SLICE_WORDS * 4 +
-               ((size_t)max_rpw * set_waves + wv) * 4;
+               ((size_t)max_rpw * set_waves + wv + set_waves) * 4;
     };
     while (sets > 1 && lds_for(sets) > 160 * 1024) --sets;
     const size_t lds = lds_for(sets);
