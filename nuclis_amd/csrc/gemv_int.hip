@@ -1439,7 +1439,9 @@ __global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t nwaves = blockDim.x >> 6;
     uint8_t *ring = (uint8_t *)lds + wv * 2 * RD_SLOT_BYTES;
-    float *partial = (float *)(lds + nwaves * 2 * (RD_SLOT_BYTES / 4));  // rows_per_wg * set_waves * NT + nwaves * 64
+    // rows_per_wg * set_waves * NT partials, 64 spare words per wave, then
+    // one row-step counter per K range
+    float *partial = (float *)(lds + nwaves * 2 * (RD_SLOT_BYTES / 4));
     const uint32_t sets = nwaves / set_waves;
     const uint32_t set = wv / set_waves, kw = wv % set_waves;
     const uint32_t slot = lane >> 3, sub = lane & 7, j = sub >> 1, c0 = 16 * (sub & 1);
@@ -1449,9 +1451,16 @@ __global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_
     const bool live = b < kb;
     const uint32_t row_begin = blockIdx.x * rows_per_wg;
     const uint32_t row_end = min(row_begin + rows_per_wg, rows);
-    const uint32_t first = row_begin + set * 4;
-    const uint32_t set_stride = sets * 4;
-    const uint32_t nsteps = first < row_end ? (row_end - first + set_stride - 1) / set_stride : 0;
+    // Step c covers rows row_begin + 4c .. 4c + 3. The waves of one K range
+    // (one per wave set) take steps set and set + sets, then claim further
+    // steps from their range's LDS counter, so waves that share a SIMD with
+    // another take fewer steps than waves alone on theirs.
+    const uint32_t first = row_begin, set_stride = 4;
+    const uint32_t tsteps = (row_end - row_begin + 3) / 4;
+    const uint32_t counters = lds_u8_addr((const uint8_t *)(partial + rows_per_wg * set_waves * NT + nwaves * 64));
+    if (threadIdx.x < set_waves) ((uint32_t *)(partial + rows_per_wg * set_waves * NT + nwaves * 64))[threadIdx.x] = 2 * sets;
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    __builtin_amdgcn_s_barrier();
 
     // DMA: lane i of copy n moves chunk 64n + i of the step (4 rows x 8 blocks)
     uint32_t dq[INSTRS], doff[INSTRS];
@@ -1471,8 +1480,9 @@ __global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_
         __builtin_amdgcn_global_load_lds((gd_global_void_t *)(wg_base + (lrow_ * stride32 + doff[n])),     \
                                          (gd_lds_void_t *)(ring + (SLOT_) * RD_SLOT_BYTES + n * 1024), 16, 0, 2); \
     }
-    NUQ_RD_DMA(0, 0u)
-    NUQ_RD_DMA(1, 1u)
+    uint32_t sid0 = set, sid1 = set + sets;
+    NUQ_RD_DMA(0, sid0)
+    NUQ_RD_DMA(1, sid1)
 
     // this lane's 16 + 16 activations of every token, and their F32 sums
     uint4 xa[NT][2], xb[NT][2];
@@ -1562,11 +1572,14 @@ __global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_
         const bool writer_ = (lane & (64 / NT - 1)) == 0 && row_ < row_end;                                 \
         partial[writer_ ? ((row_ - row_begin) * set_waves + kw) * NT + lane / (64 / NT) : spare + lane] = tot_; \
     }
-    // Step i lives in ring slot i % 2; a slot is refilled with step i + 2
-    // once its 4 rows are read.
-#define NUQ_RD_STEP(SLOT_, STEP_, VM_, REFILL_)                                                              \
+    // Each ring slot holds one step; once its 4 rows are read the slot is
+    // refilled with the wave's next claimed step. The claim (an LDS atomic
+    // in asm: as a compiler atomic it would first wait for every copy in
+    // flight) is issued before the step's reads, whose waits cover it.
+#define NUQ_RD_STEP(SLOT_, STEP_, VM_, CLAIM_, REFILL_)                                                      \
     {                                                                                                        \
         asm volatile("s_waitcnt vmcnt(%0)" : : "n"(VM_) : "memory");                                        \
+        CLAIM_                                                                                               \
         NUQ_RD_READ(SLOT_, 0)                                                                                \
         NUQ_RD_ROW(SLOT_, STEP_, 0, NUQ_RD_READ(SLOT_, 1))                                                   \
         NUQ_RD_ROW(SLOT_, STEP_, 1, NUQ_RD_READ(SLOT_, 2))                                                   \
@@ -1575,17 +1588,33 @@ __global__ void __launch_bounds__(rd_threads<NT>()) rows_dma_kernel(const uint8_
         asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); /* the slot's reads are done */                \
         REFILL_                                                                                              \
     }
+#define NUQ_RD_CLAIM                                                                                         \
+    if (lane == 0) asm volatile("ds_add_rtn_u32 %0, %1, %2" : "=v"(c_) : "v"(claim_addr), "v"(1u) : "memory");
+#define NUQ_RD_NEXT(SLOT_, SID_)                                                                             \
+    asm volatile("" : "+v"(c_));                                                                             \
+    c_ = __builtin_amdgcn_readfirstlane(c_);                                                                 \
+    if (c_ < tsteps) {                                                                                       \
+        NUQ_RD_DMA(SLOT_, c_)                                                                                \
+    } else {                                                                                                 \
+        claiming = false;                                                                                    \
+    }                                                                                                        \
+    SID_ = c_;
     // the x loads were issued after the first two steps' copies: wait for all
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-    uint32_t i = 0;
-    for (; i + 4 <= nsteps; i += 2) {
-        NUQ_RD_STEP(0, i, INSTRS, NUQ_RD_DMA(0, i + 2))
-        NUQ_RD_STEP(1, i + 1, INSTRS, NUQ_RD_DMA(1, i + 3))
+    const uint32_t claim_addr = counters + 4 * kw;
+    bool claiming = sid0 < tsteps && sid1 < tsteps;
+    while (claiming) {
+        uint32_t c_ = 0;
+        NUQ_RD_STEP(0, sid0, INSTRS, NUQ_RD_CLAIM, NUQ_RD_NEXT(0, sid0))
+        if (!claiming) break;
+        c_ = 0;
+        NUQ_RD_STEP(1, sid1, INSTRS, NUQ_RD_CLAIM, NUQ_RD_NEXT(1, sid1))
     }
-    if (i < nsteps) NUQ_RD_STEP(0, i, 0, if (i + 2 < nsteps) { NUQ_RD_DMA(0, i + 2) })
-    if (i + 1 < nsteps) NUQ_RD_STEP(1, i + 1, 0, if (i + 3 < nsteps) { NUQ_RD_DMA(1, i + 3) })
-    if (i + 2 < nsteps) NUQ_RD_STEP(0, i + 2, 0, )
-    if (i + 3 < nsteps) NUQ_RD_STEP(1, i + 3, 0, )
+    // the steps still held, with full waits (fewer copies are in flight)
+    if (sid0 < tsteps) NUQ_RD_STEP(0, sid0, 0, , )
+    if (sid1 < tsteps) NUQ_RD_STEP(1, sid1, 0, , )
+#undef NUQ_RD_NEXT
+#undef NUQ_RD_CLAIM
 #undef NUQ_RD_STEP
 #undef NUQ_RD_ROW
 #undef NUQ_RD_READ
@@ -1635,7 +1664,8 @@ bool launch_rows_q4k_f16(hipStream_t s, const uint8_t *w, uint64_t stride, uint3
     const uint32_t wgs = std::max(1u, 256 / ranges);
     const uint32_t rows_per_wg = std::max(4u, (rows + wgs - 1) / wgs);
     if ((uint64_t)rows_per_wg * stride > 0xffffffffull) return false;
-    const size_t lds = (size_t)nwaves * 2 * RD_SLOT_BYTES + ((size_t)rows_per_wg * set_waves * nt + nwaves * 64) * 4;
+    const size_t lds =
+        (size_t)nwaves * 2 * RD_SLOT_BYTES + ((size_t)rows_per_wg * set_waves * nt + nwaves * 64 + set_waves) * 4;
     if (lds > 160 * 1024) return false;
     const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg, ranges), block(64 * nwaves);
     float *out = ranges > 1 ? ws : y;
