@@ -978,3 +978,32 @@ def test_register_rows_kernel_graph_replays_match_eager(backend, rows, columns, 
         backend.matmul_kernel(nq.KERNEL_ROWS, m, xg, columns, other, rows, tokens)
         backend.sync()
         assert torch.equal(other.view(torch.int32), eager.view(torch.int32))
+
+
+@pytest.mark.parametrize("encoding,rows,columns", [(12, 17408, 5120), (12, 4096, 4096), (8, 4096, 4096),
+                                                    (13, 17408, 5120), (14, 20000, 5120), (23, 17408, 5120),
+                                                    (12, 333, 5120)])
+def test_matvec_repeats_bit_identically(backend, encoding, rows, columns):
+    """Within a workgroup of the DMA GEMV, the waves of one K range claim row
+    steps at run time, so which wave computes a row changes from launch to
+    launch; a row's sum must not. Five launches, with another matrix's GEMV
+    between them, give the same bits as the first (and match the oracle)."""
+    import torch
+    w = quantized(encoding, rows, columns, 170)
+    xh = gaussian(171, columns)
+    m = nq.Matrix(encoding, rows, columns, to_gpu(w))
+    other = nq.Matrix(encoding, 2048, columns, to_gpu(quantized(encoding, 2048, columns, 172)))
+    x = to_gpu(xh)
+    print(f"[repeat] enc {encoding} {rows}x{columns}", flush=True)
+    first = torch.empty(rows, device="cuda")
+    backend.matvec(m, x, first)
+    sink = torch.empty(2048, device="cuda")
+    for _ in range(5):
+        backend.matvec(other, x, sink)
+        again = torch.full((rows,), np.nan, device="cuda")
+        backend.matvec(m, x, again)
+        backend.sync()
+        assert torch.equal(again.view(torch.int32), first.view(torch.int32))
+    want = orc.matvec(encoding, rows, columns, w, xh)
+    check_close(first.cpu().numpy(), want, mass(encoding, w, rows, columns, xh)[0], F32_K,
+                f"repeat {encoding} {rows}x{columns}")
