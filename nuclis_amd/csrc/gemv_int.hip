@@ -1126,7 +1126,11 @@ static hipError_t launch_dma(hipStream_t s, const uint8_t *w, uint64_t stride, u
     // and each wave streams at least two steps: Q8_0 4096 x 4096 (16 rows
     // per workgroup) took 6.1 us with four sets of one step and 5.5 us with
     // two or one on MI355X. The wider shapes stay at their LDS-bound cap.
-    if (!sets_wanted) sets_wanted = std::max(1u, rows / (2 * cus * step_rows));
+    // Q8_0 and Q6_K prefer half as many sets again (about four steps per
+    // wave): Q8_0 4096 x 4096 5.73 -> 5.46 us, 8192 x 4096 8.9 -> 8.5, Q6_K
+    // 4096 x 4096 6.24 -> 5.9; Q4_K, Q5_K and IQ4_XS measured 2-4 % slower so.
+    const uint32_t per_set = (ENC == 8 || ENC == 14 ? 4 : 2) * cus * step_rows;
+    if (!sets_wanted) sets_wanted = std::max(1u, rows / per_set);
     if (sets_wanted < sets) sets = sets_wanted;
     // Rows per workgroup need not be whole set steps (each set guards its
     // last step), so the grid is the CU count and each CU streams the same
