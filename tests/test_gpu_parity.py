@@ -982,7 +982,8 @@ def test_register_rows_kernel_graph_replays_match_eager(backend, rows, columns, 
 
 @pytest.mark.parametrize("encoding,rows,columns", [(12, 17408, 5120), (12, 4096, 4096), (8, 4096, 4096),
                                                     (13, 17408, 5120), (14, 20000, 5120), (23, 17408, 5120),
-                                                    (12, 333, 5120)])
+                                                    (12, 333, 5120), (12, 1, 5120), (12, 5, 5120), (12, 129, 5120),
+                                                    (8, 3, 4096), (14, 17, 5120), (12, 2049, 2560)])
 def test_matvec_repeats_bit_identically(backend, encoding, rows, columns):
     """Within a workgroup of the DMA GEMV, the waves of one K range claim row
     steps at run time, so which wave computes a row changes from launch to
